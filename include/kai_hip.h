@@ -1,0 +1,75 @@
+/*
+ * kai_hip: C ABI of the MI355X (gfx950) GGUF dequant-fused quantized linear.
+ *
+ * Drop-in for the exports that the reference's Python bridge binds with ctypes
+ * (vllm_gguf_plugin/quantization/native_fused.py:52-85) from its CUDA library
+ * (vllm_gguf_plugin/native/kernels/current_ggml_direct.cu). Same names, argument
+ * order and meaning, status conventions:
+ *   - every pointer is device memory owned by the caller (PyTorch); the library
+ *     performs no allocation, copy or synchronisation on these entry points;
+ *   - `stream` is a hipStream_t passed as uintptr_t; 0 is the null stream;
+ *   - activation dtype codes: 0 = f32, 1 = bf16, 2 = f16;
+ *   - int entry points return 0 on success and -1 on error, size queries return
+ *     0 on error; the message is kept per host thread (current_direct_error);
+ *   - weight types are GGML ids: Q4_0 = 2, Q8_0 = 8, Q2_K = 10, Q4_K = 12,
+ *     Q6_K = 14, IQ3_S = 21; weights are the unchanged GGUF wire bytes, row-major
+ *     [n, (k / qk) * block_bytes];
+ *   - the activation buffer is [pass1: m*(k/32) Q8_1 blocks of 36 bytes, padded to
+ *     256][pass2 when two_pass][inverse: m floats, padded to 256].
+ */
+#ifndef KAI_HIP_H
+#define KAI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Last error message of the calling thread ("" after a successful call).
+ * Replaces current_direct_error (current_ggml_direct.cu:174). */
+const char *current_direct_error(void);
+
+/* 1 when kai_fused_mmvq can run this shape: supported type, 1 <= m <= 8,
+ * k % 32 == 0, k / 32 <= 1024, k % qk == 0, 0 < n <= INT_MAX; else 0.
+ * Replaces kai_fused_supported (current_ggml_direct.cu:826-835). */
+int kai_fused_supported(int type, int64_t n, int64_t k, int64_t m);
+
+/* Bytes of the activation buffer for m rows of k values.
+ * Replaces kai_fused_activation_bytes (current_ggml_direct.cu:837-839). */
+size_t kai_fused_activation_bytes(int64_t m, int64_t k, int two_pass);
+
+/* Q8_1 activation preparation of x [m, k] (row stride stride_x elements) into
+ * `activation`: exact power-of-two row normalisation, then per-32-value Q8_1.
+ * Replaces kai_fused_prepare (current_ggml_direct.cu:841-863; kernel
+ * kai_dual_mmvq.cuh:147-254). */
+int kai_fused_prepare(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x,
+                      void *activation, int two_pass, uintptr_t stream);
+
+/* GEMV: dst[j * stride_dst + r] = inverse[j] * sum_b dot(W[r, b], q8[j, b]) for
+ * r < n, j < m <= 8; F32 or BF16 (dst_bf16) output.
+ * Replaces kai_fused_mmvq (current_ggml_direct.cu:946-965; kernel kai_dual_mmvq.cuh:258-397). */
+int kai_fused_mmvq(const void *weight, int type, int64_t n, int64_t k, int64_t m,
+                   const void *activation, int two_pass, void *dst, int dst_bf16,
+                   int64_t stride_dst, uintptr_t stream);
+
+/* Scratch bytes kai_fused_mmq_run needs for `count` matrices (types[i], rows[i])
+ * sharing k, at m > 8 activation rows. direct_f32 is accepted for signature
+ * compatibility. Replaces kai_fused_mmq_workspace (current_ggml_direct.cu:1196-1205). */
+size_t kai_fused_mmq_workspace(int device, const int *types, const int64_t *rows, int count,
+                               int64_t k, int64_t m, int direct_f32);
+
+/* Batched projection group for m > 8 rows (multi-sequence decode, spec-verify,
+ * prefill): one activation preparation, then every matrix writes its column
+ * slice of dst [m, sum rows] (row stride stride_dst, or sum rows when 0); F32 or
+ * BF16. Replaces kai_fused_mmq_run (current_ggml_direct.cu:1207-1265). */
+int kai_fused_mmq_run(const void *const *weights, const int *types, const int64_t *rows, int count,
+                      const void *x, int x_dtype, int64_t stride_x, int64_t k, int64_t m,
+                      void *dst, int dst_bf16, int64_t stride_dst, void *scratch, size_t scratch_bytes,
+                      int device, uintptr_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,160 @@
+// C ABI (include/kai_hip.h): argument validation, buffer layout and dispatch.
+// Mirrors the reference's exports in current_ggml_direct.cu:808-1265 — same
+// names, arguments, status codes and thread-local error message — with every
+// launch going to the gfx950 kernels of this library.
+#include <algorithm>
+#include <climits>
+#include <string>
+
+#include "../../include/kai_hip.h"
+#include "kai_launch.h"
+
+namespace {
+
+thread_local std::string last_error;
+
+struct Layout {
+    kai::block_q8_1 *y1;
+    kai::block_q8_1 *y2;
+    float *inverse;
+};
+
+Layout activation_layout(void *activation, int64_t m, int64_t k, int two_pass) {
+    char *base = static_cast<char *>(activation);
+    const size_t pass = kai::q8_1_pass_bytes(m, k);
+    return {reinterpret_cast<kai::block_q8_1 *>(base),
+            two_pass ? reinterpret_cast<kai::block_q8_1 *>(base + pass) : nullptr,
+            reinterpret_cast<float *>(base + pass * (two_pass ? 2 : 1))};
+}
+
+size_t activation_bytes(int64_t m, int64_t k, int two_pass) {
+    return kai::q8_1_pass_bytes(m, k) * (two_pass ? 2 : 1) + kai::align256(size_t(m) * sizeof(float));
+}
+
+constexpr int MAX_FUSED_ROWS = 8;  // kai_fused_mmvq contract (reference MAX_COLS)
+constexpr int MAX_K_BLOCKS = 1024;  // k <= 32768, one preparation lane per 32 values
+constexpr int MAX_GROUP = 32;       // matrices per projection group
+
+bool shape_ok(int type, int64_t n, int64_t k, int64_t m, int64_t max_m) {
+    const int qk = kai::block_elems(type);
+    return kai::weight_type_supported(type) && n > 0 && n <= INT_MAX && k > 0 && k <= INT_MAX && m >= 1 &&
+           m <= max_m && k % kai::QK8_1 == 0 && k / kai::QK8_1 <= MAX_K_BLOCKS && k % qk == 0;
+}
+
+hipStream_t stream_of(uintptr_t raw) { return reinterpret_cast<hipStream_t>(raw); }
+
+template <typename F>
+int entry(F &&body) {
+    try {
+        last_error.clear();
+        body();
+        const hipError_t status = hipGetLastError();
+        if (status != hipSuccess) throw kai::Error(hipGetErrorString(status));
+        return 0;
+    } catch (const std::exception &error) {
+        last_error = error.what();
+        return -1;
+    }
+}
+
+struct Group {
+    int64_t total_rows = 0;
+};
+
+Group validate_group(const int *types, const int64_t *rows, int count, int64_t k, int64_t m) {
+    if (!types || !rows || count < 1 || count > MAX_GROUP)
+        throw kai::Error("Expected between one and 32 original GGUF matrices");
+    if (m <= MAX_FUSED_ROWS || m > INT_MAX) throw kai::Error("Fused MMQ requires more than 8 activation rows");
+    Group g;
+    for (int i = 0; i < count; ++i) {
+        if (!shape_ok(types[i], rows[i], k, m, INT_MAX)) throw kai::Error("Invalid fused MMQ matrix type or shape");
+        g.total_rows += rows[i];
+    }
+    if (g.total_rows % 4 || g.total_rows > INT_MAX) throw kai::Error("Fused MMQ output width must be a multiple of four");
+    return g;
+}
+
+}  // namespace
+
+extern "C" const char *current_direct_error(void) { return last_error.c_str(); }
+
+extern "C" int kai_fused_supported(int type, int64_t n, int64_t k, int64_t m) {
+    return shape_ok(type, n, k, m, MAX_FUSED_ROWS) ? 1 : 0;
+}
+
+extern "C" size_t kai_fused_activation_bytes(int64_t m, int64_t k, int two_pass) {
+    if (m < 1 || k < 0) return 0;
+    return activation_bytes(m, k, two_pass);
+}
+
+extern "C" int kai_fused_prepare(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x,
+                                 void *activation, int two_pass, uintptr_t stream) {
+    return entry([&] {
+        if (!x || !activation || m < 1 || m > INT_MAX || k <= 0 || k % kai::QK8_1 || k > INT_MAX || stride_x < k)
+            throw kai::Error("Invalid fused activation preparation arguments");
+        const Layout l = activation_layout(activation, m, k, two_pass);
+        kai::launch_prepare(x, x_dtype, m, k, stride_x, l.y1, l.y2, l.inverse, stream_of(stream));
+    });
+}
+
+extern "C" int kai_fused_mmvq(const void *weight, int type, int64_t n, int64_t k, int64_t m,
+                              const void *activation, int two_pass, void *dst, int dst_bf16, int64_t stride_dst,
+                              uintptr_t stream) {
+    return entry([&] {
+        if (!weight || !activation || !dst || !shape_ok(type, n, k, m, MAX_FUSED_ROWS) || stride_dst < n ||
+            stride_dst > INT_MAX)
+            throw kai::Error("Invalid fused MMVQ arguments");
+        const Layout l = activation_layout(const_cast<void *>(activation), m, k, two_pass);
+        kai::launch_mmvq(type, weight, n, k, m, l.y1, l.y2, l.inverse, dst, dst_bf16 != 0, stride_dst,
+                         stream_of(stream));
+    });
+}
+
+extern "C" size_t kai_fused_mmq_workspace(int device, const int *types, const int64_t *rows, int count, int64_t k,
+                                          int64_t m, int direct_f32) {
+    (void)direct_f32;
+    try {
+        last_error.clear();
+        if (device < 0) throw kai::Error("Invalid device index");
+        validate_group(types, rows, count, k, m);
+        return activation_bytes(m, k, 0);
+    } catch (const std::exception &error) {
+        last_error = error.what();
+        return 0;
+    }
+}
+
+extern "C" int kai_fused_mmq_run(const void *const *weights, const int *types, const int64_t *rows, int count,
+                                 const void *x, int x_dtype, int64_t stride_x, int64_t k, int64_t m, void *dst,
+                                 int dst_bf16, int64_t stride_dst, void *scratch, size_t scratch_bytes, int device,
+                                 uintptr_t stream) {
+    return entry([&] {
+        const Group g = validate_group(types, rows, count, k, m);
+        const size_t need = activation_bytes(m, k, 0);
+        if (!weights || !x || !dst || !scratch || scratch_bytes < need || k % 4 || stride_x < k || device < 0)
+            throw kai::Error("Invalid fused MMQ pointers, strides or scratch capacity");
+        for (int i = 0; i < count; ++i)
+            if (!weights[i]) throw kai::Error("Null packed matrix");
+        const int64_t ld = stride_dst ? stride_dst : g.total_rows;
+        if (ld < g.total_rows) throw kai::Error("Fused MMQ output stride is smaller than the output width");
+        int current = -1;
+        if (hipGetDevice(&current) != hipSuccess) throw kai::Error("No HIP device");
+        if (current != device && hipSetDevice(device) != hipSuccess) throw kai::Error("Invalid device index");
+        const hipStream_t s = stream_of(stream);
+        const Layout l = activation_layout(scratch, m, k, 0);
+        kai::launch_prepare(x, x_dtype, m, k, stride_x, l.y1, nullptr, l.inverse, s);
+        const int64_t yrb = k / kai::QK8_1;
+        const size_t elem = dst_bf16 ? 2 : 4;
+        int64_t col = 0;
+        for (int i = 0; i < count; ++i) {
+            for (int64_t j0 = 0; j0 < m; j0 += kai::MMVQ_MAX_ROWS) {
+                const int64_t mm = std::min<int64_t>(kai::MMVQ_MAX_ROWS, m - j0);
+                char *out = static_cast<char *>(dst) + (j0 * ld + col) * elem;
+                kai::launch_mmvq(types[i], weights[i], rows[i], k, mm, l.y1 + j0 * yrb, nullptr, l.inverse + j0, out,
+                                 dst_bf16 != 0, ld, s);
+            }
+            col += rows[i];
+        }
+        if (current != device) (void)hipSetDevice(current);
+    });
+}

@@ -1,0 +1,154 @@
+// Q8_1 activation preparation (kernel "prepare"): exact per-row power-of-two
+// normalisation followed by Q8_1 quantisation of every 32-value block.
+//
+// Follows kai_dual::prepare_dual (vllm_gguf_plugin/native/kernels/kai_dual_mmvq.cuh:147-254):
+//   amax = max |x| over the row; e = biased exponent of amax;
+//   se = clamp(260 - e, 1, 253) when 0 < e < 255, else 127;
+//   scale = 2^(se - 127) puts amax into [64, 128); inverse[row] = 2^(127 - se);
+//   per block: v = x * scale, a = max|v|, d = a / 127, q = a == 0 ? 0 : roundf(v / d),
+//   ds = (half_rn(d), half_rn(d * sum q)).
+//   two_pass adds a second block quantising v - half(d) * q (one fused multiply-add).
+// Division is IEEE (hipcc's default correctly rounded fp32 divide), so the
+// bytes are identical to the CPU restatement.
+//
+// Launch: one workgroup per activation row, one lane per 32-value block, the row
+// read once into registers; wave64 reductions for the row maximum.
+#include "kai_launch.h"
+
+namespace kai {
+
+constexpr int PREP_MAX_THREADS = 1024;  // K <= 32768
+
+template <int DTYPE>
+__device__ __forceinline__ void load_block32(const typename Src<DTYPE>::T *p, float (&v)[32]) {
+    if constexpr (DTYPE == 0) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const float4 f = load_unaligned<float4>(p + 4 * c);
+            v[4 * c + 0] = f.x; v[4 * c + 1] = f.y; v[4 * c + 2] = f.z; v[4 * c + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint4 u = load_unaligned<uint4>(p + 8 * c);
+            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t lo = w[i] & 0xffffu, hi = w[i] >> 16;
+                if constexpr (DTYPE == 1) {
+                    v[8 * c + 2 * i] = bf16_bits_to_float(lo);
+                    v[8 * c + 2 * i + 1] = bf16_bits_to_float(hi);
+                } else {
+                    v[8 * c + 2 * i] = half_bits_to_float(lo);
+                    v[8 * c + 2 * i + 1] = half_bits_to_float(hi);
+                }
+            }
+        }
+    }
+}
+
+// Quantise 32 normalised values into one Q8_1 block; returns the stored fp16 d.
+__device__ __forceinline__ float quantize_block(const float (&v)[32], block_q8_1 *out, int8_t (&q)[32]) {
+    float a = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) a = fmaxf(a, fabsf(v[j]));
+    const float d = a / 127.0f;
+    int isum = 0;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        q[j] = static_cast<int8_t>(a == 0.0f ? 0.0f : roundf(v[j] / d));
+        isum += q[j];
+    }
+    const uint16_t hd = float_to_half_bits(d);
+    const uint16_t hs = float_to_half_bits(d * static_cast<float>(isum));
+    uint32_t words[9];
+    words[0] = static_cast<uint32_t>(hd) | (static_cast<uint32_t>(hs) << 16);
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+        words[1 + w] = static_cast<uint32_t>(static_cast<uint8_t>(q[4 * w])) |
+                       (static_cast<uint32_t>(static_cast<uint8_t>(q[4 * w + 1])) << 8) |
+                       (static_cast<uint32_t>(static_cast<uint8_t>(q[4 * w + 2])) << 16) |
+                       (static_cast<uint32_t>(static_cast<uint8_t>(q[4 * w + 3])) << 24);
+    }
+    __builtin_memcpy(out, words, sizeof(words));  // 36 bytes, 4-byte aligned
+    return half_bits_to_float(hd);
+}
+
+// Row scale from the row maximum: returns scale, writes inverse through lane 0.
+__device__ __forceinline__ float row_scale_from_max(float amax, float *inverse_out, bool writer) {
+    const int biased = static_cast<int>((__builtin_bit_cast(uint32_t, amax) >> 23) & 255u);
+    int se = 127;
+    if (biased != 0 && biased != 255) se = min(max(260 - biased, 1), 253);
+    if (writer) *inverse_out = __builtin_bit_cast(float, static_cast<uint32_t>(254 - se) << 23);
+    return __builtin_bit_cast(float, static_cast<uint32_t>(se) << 23);
+}
+
+// Block-wide maximum over up to 16 waves; all lanes get the result.
+__device__ __forceinline__ float block_max(float v, float *lds) {
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    v = wave_max(v);
+    if (lane == 0) lds[wave] = v;
+    __syncthreads();
+    const int nwaves = (blockDim.x + WAVE - 1) / WAVE;
+    float m = 0.0f;
+    for (int w = 0; w < nwaves; ++w) m = fmaxf(m, lds[w]);
+    return m;
+}
+
+template <int DTYPE, bool TWO_PASS>
+__global__ __launch_bounds__(PREP_MAX_THREADS) void prepare_q8_1_kernel(
+    const typename Src<DTYPE>::T *__restrict__ x, int64_t stride_x, int k, block_q8_1 *__restrict__ y1,
+    block_q8_1 *__restrict__ y2, float *__restrict__ inverse) {
+    __shared__ float wave_max_lds[PREP_MAX_THREADS / WAVE];
+    const int row = blockIdx.x;
+    const int ib = threadIdx.x;
+    const int nblocks = k / QK8_1;
+    float v[32];
+    float bmax = 0.0f;
+    if (ib < nblocks) {
+        load_block32<DTYPE>(x + static_cast<int64_t>(row) * stride_x + static_cast<int64_t>(ib) * QK8_1, v);
+#pragma unroll
+        for (int j = 0; j < 32; ++j) bmax = fmaxf(bmax, fabsf(v[j]));
+    }
+    const float amax = block_max(bmax, wave_max_lds);
+    const float scale = row_scale_from_max(amax, inverse + row, threadIdx.x == 0);
+    if (ib >= nblocks) return;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) v[j] *= scale;
+    int8_t q1[32];
+    const float d1h = quantize_block(v, y1 + static_cast<int64_t>(row) * nblocks + ib, q1);
+    if constexpr (TWO_PASS) {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) v[j] = fmaf(-d1h, static_cast<float>(q1[j]), v[j]);
+        int8_t q2[32];
+        quantize_block(v, y2 + static_cast<int64_t>(row) * nblocks + ib, q2);
+    }
+}
+
+template <int DTYPE>
+static void launch_prepare_dtype(const void *x, int64_t m, int64_t k, int64_t stride_x, block_q8_1 *y1,
+                                 block_q8_1 *y2, float *inverse, hipStream_t stream) {
+    const int nblocks = static_cast<int>(k / QK8_1);
+    const int threads = (nblocks + WAVE - 1) / WAVE * WAVE;
+    const auto *src = static_cast<const typename Src<DTYPE>::T *>(x);
+    if (y2) {
+        prepare_q8_1_kernel<DTYPE, true><<<dim3(static_cast<unsigned>(m)), dim3(threads), 0, stream>>>(
+            src, stride_x, static_cast<int>(k), y1, y2, inverse);
+    } else {
+        prepare_q8_1_kernel<DTYPE, false><<<dim3(static_cast<unsigned>(m)), dim3(threads), 0, stream>>>(
+            src, stride_x, static_cast<int>(k), y1, y2, inverse);
+    }
+}
+
+void launch_prepare(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, block_q8_1 *y1,
+                    block_q8_1 *y2, float *inverse, hipStream_t stream) {
+    if (k / QK8_1 > PREP_MAX_THREADS) throw Error("Fused activation preparation supports K <= 32768");
+    switch (x_dtype) {
+        case 0: launch_prepare_dtype<0>(x, m, k, stride_x, y1, y2, inverse, stream); break;
+        case 1: launch_prepare_dtype<1>(x, m, k, stride_x, y1, y2, inverse, stream); break;
+        case 2: launch_prepare_dtype<2>(x, m, k, stride_x, y1, y2, inverse, stream); break;
+        default: throw Error("Fused activations must be F32, BF16 or F16");
+    }
+}
+
+}  // namespace kai

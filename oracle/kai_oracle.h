@@ -1,0 +1,85 @@
+/*
+ * CPU oracle for the GGUF dequant-fused quantized linear path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker
+ * (or, for the baseline, as the timed CPU restatement). The product library
+ * (kaillm_amd/libkai_hip.so) never links or calls it.
+ *
+ * It restates, in plain C with IEEE float arithmetic, what the reference path
+ * computes:
+ *   - Q8_1 activation preparation of kai_dual::prepare_dual
+ *     (vllm_gguf_plugin/native/kernels/kai_dual_mmvq.cuh:147-254) and the
+ *     activation buffer layout of current_ggml_direct.cu:808-839;
+ *   - the per-format block dot products vec_dot_{q8_0,q4_0,q4_K,q6_K,q2_K,iq3_s}_q8_1
+ *     (llama.cpp @0c1e570, not vendored; in-tree text csrc/gguf/vecdotq.cuh), evaluated
+ *     as exact integer block sums times the stored fp16 scales, accumulated in FP64;
+ *   - the GEMV epilogue y[j, r] = inverse[j] * sum_b dot(W[r, b], q8[j, b])
+ *     (kai_dual_mmvq.cuh:258-327);
+ *   - block dequantization per gguf-py quants.py (:242-252, :397-402, :407-429,
+ *     :476-523, :553-573, :1097-1125).
+ * Each function names the reference lines it follows.
+ *
+ * Pinning (tests/test_oracle_*.py): fp16/bf16 conversion against numpy; Q8_1
+ * preparation against closed-form special cases and invariants; dequantization
+ * against hand-assembled known-answer blocks; the block dots against
+ * dequantize-then-dot in FP64 (an independent route through the layout); the
+ * IQ3_S grid against the older vendored table (tests/golden/gen_iq3s_grid.py).
+ */
+#ifndef KAI_ORACLE_H
+#define KAI_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    ORACLE_Q4_0 = 2,
+    ORACLE_Q8_0 = 8,
+    ORACLE_Q8_1 = 9,
+    ORACLE_Q2_K = 10,
+    ORACLE_Q4_K = 12,
+    ORACLE_Q6_K = 14,
+    ORACLE_IQ3_S = 21,
+};
+
+/* Elements and bytes per block; 0 for an unsupported type. */
+int oracle_block_elems(int type);
+int oracle_block_bytes(int type);
+
+/* IEEE half <-> float (round to nearest even), bf16 -> float. */
+float oracle_half_to_float(uint16_t h);
+uint16_t oracle_float_to_half(float f);
+float oracle_bf16_to_float(uint16_t b);
+
+/* Activation buffer bytes: [pass1 m*(k/32)*36, 256-aligned][pass2][inverse m*4, 256-aligned]. */
+size_t oracle_activation_bytes(int64_t m, int64_t k, int two_pass);
+
+/* Q8_1 activation preparation. x_dtype: 0 f32, 1 bf16, 2 f16. Returns 0 or -1. */
+int oracle_prepare(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x,
+                   void *activation, int two_pass);
+
+/* Dequantize one row of k elements. Returns 0 or -1. */
+int oracle_dequantize_row(int type, const uint8_t *row, int64_t k, float *out);
+
+/* Block dot of weight row r (n rows, k columns) with activation row j, FP64.
+ * out[j * n + r] = inverse[j] * sum_b dot(...) (+ pass 2 when two_pass). */
+int oracle_mul_mat(int type, const uint8_t *weight, int64_t n, int64_t k, int64_t m,
+                   const void *activation, int two_pass, double *out, int threads);
+
+/* Same arithmetic as oracle_mul_mat, written to float out with stride. Used as the
+ * CPU baseline timing leg. */
+int oracle_mul_mat_f32(int type, const uint8_t *weight, int64_t n, int64_t k, int64_t m,
+                       const void *activation, int two_pass, float *out, int64_t stride_out,
+                       int threads);
+
+/* Library identity string (build flags), for reports. */
+const char *oracle_build_info(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

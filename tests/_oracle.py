@@ -1,0 +1,138 @@
+"""numpy wrappers around the CPU oracle (oracle/liboracle.so) — the checker.
+
+Test infrastructure only; the product (kaillm_amd) never imports this.
+"""
+import ctypes
+import subprocess
+from functools import lru_cache
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parents[1]
+ORACLE_SO = ROOT / "oracle" / "liboracle.so"
+
+Q4_0, Q8_0, Q8_1, Q2_K, Q4_K, Q6_K, IQ3_S = 2, 8, 9, 10, 12, 14, 21
+WEIGHT_TYPES = (Q8_0, Q4_0, Q4_K, Q6_K, Q2_K, IQ3_S)
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q8_1: (32, 36), Q2_K: (256, 84), Q4_K: (256, 144),
+         Q6_K: (256, 210), IQ3_S: (256, 110)}
+NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q2_K: "Q2_K", Q4_K: "Q4_K", Q6_K: "Q6_K", IQ3_S: "IQ3_S"}
+
+
+@lru_cache(maxsize=1)
+def lib():
+    if not ORACLE_SO.is_file():
+        subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], check=True)
+    o = ctypes.CDLL(str(ORACLE_SO))
+    i64, ptr, c_int = ctypes.c_int64, ctypes.c_void_p, ctypes.c_int
+    o.oracle_half_to_float.argtypes = [ctypes.c_uint16]
+    o.oracle_half_to_float.restype = ctypes.c_float
+    o.oracle_float_to_half.argtypes = [ctypes.c_float]
+    o.oracle_float_to_half.restype = ctypes.c_uint16
+    o.oracle_activation_bytes.argtypes = [i64, i64, c_int]
+    o.oracle_activation_bytes.restype = ctypes.c_size_t
+    o.oracle_prepare.argtypes = [ptr, c_int, i64, i64, i64, ptr, c_int]
+    o.oracle_prepare.restype = c_int
+    o.oracle_dequantize_row.argtypes = [c_int, ptr, i64, ptr]
+    o.oracle_dequantize_row.restype = c_int
+    o.oracle_mul_mat.argtypes = [c_int, ptr, i64, i64, i64, ptr, c_int, ptr, c_int]
+    o.oracle_mul_mat.restype = c_int
+    o.oracle_mul_mat_f32.argtypes = [c_int, ptr, i64, i64, i64, ptr, c_int, ptr, i64, c_int]
+    o.oracle_mul_mat_f32.restype = c_int
+    o.oracle_build_info.restype = ctypes.c_char_p
+    return o
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+DTYPE_CODE = {np.float32: 0, "bf16": 1, np.float16: 2}
+
+
+def activation_bytes(m, k, two_pass=0):
+    return lib().oracle_activation_bytes(m, k, two_pass)
+
+
+def prepare(x, two_pass=0, dtype_code=None, stride=None):
+    """x: float32 [m,k] (code 0), float16 (code 2) or uint16 bf16 bits (code 1)."""
+    x = np.ascontiguousarray(x)
+    if dtype_code is None:
+        dtype_code = 0 if x.dtype == np.float32 else 2 if x.dtype == np.float16 else 1
+    m, cols = x.shape
+    k = cols if stride is None else stride[1]
+    stride_x = cols
+    out = np.zeros(activation_bytes(m, k, two_pass), dtype=np.uint8)
+    assert lib().oracle_prepare(_p(x), dtype_code, m, k, stride_x, _p(out), two_pass) == 0
+    return out
+
+
+def split_activation(buf, m, k, two_pass=0):
+    """-> (d [m, k/32] f32, s [m, k/32] f32, q [m, k] int8, inverse [m] f32, pass-2 tuple or None)."""
+    nb = k // 32
+    pass_bytes = (m * nb * 36 + 255) // 256 * 256
+
+    def one(off):
+        blocks = buf[off:off + m * nb * 36].reshape(m, nb, 36)
+        d = blocks[:, :, 0:2].copy().view(np.float16).reshape(m, nb).astype(np.float32)
+        s = blocks[:, :, 2:4].copy().view(np.float16).reshape(m, nb).astype(np.float32)
+        q = blocks[:, :, 4:].copy().view(np.int8).reshape(m, k)
+        return d, s, q
+
+    d, s, q = one(0)
+    p2 = one(pass_bytes) if two_pass else None
+    inv_off = pass_bytes * (2 if two_pass else 1)
+    inverse = buf[inv_off:inv_off + 4 * m].copy().view(np.float32)
+    return d, s, q, inverse, p2
+
+
+def dequantize(qtype, w, k):
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    n = w.shape[0]
+    out = np.empty((n, k), dtype=np.float32)
+    for r in range(n):
+        assert lib().oracle_dequantize_row(qtype, _p(w[r]), k, _p(out[r])) == 0
+    return out
+
+
+def mul_mat(qtype, w, k, activation, m, two_pass=0, threads=8):
+    """Reference GEMV/GEMM in FP64: out [m, n]."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    n = w.shape[0]
+    out = np.empty((m, n), dtype=np.float64)
+    assert lib().oracle_mul_mat(qtype, _p(w), n, k, m, _p(activation), two_pass, _p(out), threads) == 0
+    return out
+
+
+def normwise_rel(y, ref):
+    """max |y - ref| / max |ref| per output row (activation row), worst row."""
+    y = np.asarray(y, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    num = np.abs(y - ref).max(axis=-1)
+    den = np.abs(ref).max(axis=-1)
+    return float(np.max(num / np.maximum(den, 1e-300)))
+
+
+def random_blocks(qtype, n, k, rng):
+    """Random but valid wire bytes: every bit pattern, with fp16 scales set to sane values."""
+    qk, bb = BLOCK[qtype]
+    nb = k // qk
+    w = rng.integers(0, 256, size=(n, nb, bb), dtype=np.uint8)
+
+    def put_half(off, lo, hi):
+        vals = rng.uniform(lo, hi, size=(n, nb)).astype(np.float16)
+        w[:, :, off:off + 2] = vals.view(np.uint8).reshape(n, nb, 2)
+
+    if qtype in (Q8_0, Q4_0):
+        put_half(0, -0.01, 0.01)
+    elif qtype == Q4_K:
+        put_half(0, 0.0, 0.002)
+        put_half(2, 0.0, 0.002)
+    elif qtype == Q6_K:
+        put_half(208, -0.002, 0.002)
+    elif qtype == Q2_K:
+        put_half(80, 0.0, 0.004)
+        put_half(82, 0.0, 0.004)
+    elif qtype == IQ3_S:
+        put_half(0, 0.0, 0.002)
+    return w.reshape(n, nb * bb)

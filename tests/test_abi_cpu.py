@@ -1,0 +1,111 @@
+"""The C ABI without a GPU: the library loads, exports every declared symbol, and
+rejects host-detectable bad arguments the way the reference does
+(current_ggml_direct.cu:826-863, 946-965, 1196-1218)."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import _oracle as O
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions():
+    names = []
+    for header in sorted((ROOT / "include").glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names += re.findall(r"^[A-Za-z_][\w\s\*]*?\b(\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_every_declared_symbol_is_exported(kai):
+    names = declared_functions()
+    assert {"kai_fused_supported", "kai_fused_prepare", "kai_fused_mmvq", "kai_fused_mmq_run"} <= set(names)
+    for name in names:
+        assert hasattr(kai, name), name
+
+
+@pytest.mark.parametrize("args,want", [
+    ((12, 34816, 5120, 1), 1), ((12, 34816, 5120, 8), 1), ((12, 34816, 5120, 9), 0),
+    ((12, 34816, 5120, 0), 0), ((12, 100, 5000, 1), 0),  # k % 256
+    ((2, 100, 48, 1), 0), ((8, 100, 32768, 1), 1), ((8, 100, 32800, 1), 0),  # k/32 <= 1024
+    ((3, 100, 256, 1), 0), ((21, 0, 256, 1), 0), ((21, 2 ** 31, 256, 1), 0), ((14, 5, 256, 4), 1),
+])
+def test_supported(kai, args, want):
+    assert kai.kai_fused_supported(*args) == want
+
+
+def test_activation_bytes_matches_layout(kai):
+    for m, k, tp in ((1, 2048, 0), (3, 5120, 1), (16, 17408, 0), (2048, 5120, 0)):
+        assert kai.kai_fused_activation_bytes(m, k, tp) == O.activation_bytes(m, k, tp)
+
+
+def test_bad_arguments_fail_before_any_launch(kai):
+    dummy = ctypes.c_void_p(16)
+    assert kai.kai_fused_prepare(None, 0, 1, 64, 64, dummy, 0, 0) == -1
+    assert b"Invalid fused activation" in kai.current_direct_error()
+    assert kai.kai_fused_prepare(dummy, 0, 1, 60, 64, dummy, 0, 0) == -1   # k % 32
+    assert kai.kai_fused_prepare(dummy, 0, 1, 64, 32, dummy, 0, 0) == -1   # stride < k
+    assert kai.kai_fused_mmvq(dummy, 12, 16, 256, 9, dummy, 0, dummy, 0, 16, 0) == -1  # m > 8
+    assert b"Invalid fused MMVQ" in kai.current_direct_error()
+    assert kai.kai_fused_mmvq(dummy, 12, 16, 256, 1, dummy, 0, dummy, 0, 15, 0) == -1  # stride < n
+    assert kai.kai_fused_mmvq(dummy, 7, 16, 256, 1, dummy, 0, dummy, 0, 16, 0) == -1   # type
+    assert kai.kai_fused_mmvq(None, 12, 16, 256, 1, dummy, 0, dummy, 0, 16, 0) == -1
+
+
+def test_mmq_workspace_rules(kai):
+    types = (ctypes.c_int * 2)(12, 14)
+    rows = (ctypes.c_int64 * 2)(34816, 5120)
+    assert kai.kai_fused_mmq_workspace(0, types, rows, 2, 5120, 16, 0) >= O.activation_bytes(16, 5120)
+    assert kai.kai_fused_mmq_workspace(0, types, rows, 2, 5120, 8, 0) == 0          # needs m > 8
+    assert b"more than 8" in kai.current_direct_error()
+    assert kai.kai_fused_mmq_workspace(0, types, rows, 0, 5120, 16, 0) == 0         # empty group
+    odd = (ctypes.c_int64 * 2)(34816, 5119)
+    assert kai.kai_fused_mmq_workspace(0, types, odd, 2, 5120, 16, 0) == 0          # sum % 4
+    assert kai.kai_fused_mmq_workspace(-1, types, rows, 2, 5120, 16, 0) == 0        # device
+    ptrs = (ctypes.c_void_p * 2)(16, 32)
+    assert kai.kai_fused_mmq_run(ptrs, types, rows, 2, ctypes.c_void_p(16), 2, 5120, 5120, 16,
+                                 ctypes.c_void_p(16), 0, 0, ctypes.c_void_p(16), 10, 0, 0) == -1
+    assert b"scratch" in kai.current_direct_error()
+
+
+@pytest.mark.parametrize("qtype", O.WEIGHT_TYPES, ids=lambda t: O.NAMES[t])
+def test_quantizer_round_trip(qtype):
+    """The host quantizer writes valid blocks whose oracle dequantization tracks the floats."""
+    from kaillm_amd.formats import quantize
+
+    rng = np.random.default_rng(qtype)
+    w = rng.normal(0, 0.02, (64, 1024)).astype(np.float32)
+    packed = quantize(w, qtype)
+    deq = O.dequantize(qtype, packed, 1024)
+    rel = np.sqrt(((deq - w) ** 2).mean() / (w ** 2).mean())
+    bound = {O.Q8_0: 0.01, O.Q4_0: 0.15, O.Q4_K: 0.12, O.Q6_K: 0.04, O.Q2_K: 0.5, O.IQ3_S: 0.35}[qtype]
+    assert rel < bound, rel
+
+
+def test_quantizer_matches_gguf_closed_forms():
+    """Q8_0 / Q4_0 follow gguf-py quants.py:382-394 / :223-239 (restated here in numpy)."""
+    from kaillm_amd.formats import quantize
+
+    rng = np.random.default_rng(3)
+    blocks = rng.normal(0, 0.02, (40, 32)).astype(np.float32)
+    d = np.abs(blocks).max(axis=1, keepdims=True) / np.float32(127)
+    with np.errstate(divide="ignore"):
+        idv = np.where(d == 0, 0, 1 / d).astype(np.float32)
+    t = blocks * idv
+    a = np.abs(t)
+    q = (np.sign(t) * (np.floor(a) + np.floor(2 * (a - np.floor(a))))).astype(np.int8)
+    want = np.concatenate([d.astype(np.float16).view(np.uint8), q.view(np.uint8)], axis=1)
+    assert np.array_equal(quantize(blocks, O.Q8_0), want)
+    imax = np.abs(blocks).argmax(axis=-1)[:, None]
+    mx = np.take_along_axis(blocks, imax, axis=-1)
+    d4 = mx / np.float32(-8)
+    with np.errstate(divide="ignore"):
+        id4 = np.where(d4 == 0, 0, 1 / d4).astype(np.float32)
+    qs = np.trunc(blocks * id4 + np.float32(8.5)).astype(np.uint8).clip(0, 15)
+    qs = qs[:, :16] | (qs[:, 16:] << 4)
+    want4 = np.concatenate([d4.astype(np.float16).view(np.uint8), qs], axis=1)
+    assert np.array_equal(quantize(blocks, O.Q4_0), want4)

@@ -1,0 +1,257 @@
+"""Parity of the gfx950 kernels with the CPU oracle, called through the C ABI.
+
+Bars: Q8_1 activation bytes bit-exact; GEMV/GEMM outputs within 1e-3 normwise
+max-rel (max|y - ref| / max|ref| per activation row) of the oracle's FP64 result
+for F32 output, and within 2^-8 for BF16 output (bf16 keeps 8 significant bits,
+so rounding alone reaches 2^-9 of max|y|).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import _oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-3
+TOL_BF16 = 2.0 ** -8
+DEV = "cuda:0"
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def to_dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def gpu_prepare(kai, x_dev, two_pass=0):
+    m, k = x_dev.shape
+    code = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[x_dev.dtype]
+    act = torch.empty(kai.kai_fused_activation_bytes(m, k, two_pass), dtype=torch.uint8, device=DEV)
+    st = kai.kai_fused_prepare(x_dev.data_ptr(), code, m, k, x_dev.stride(0), act.data_ptr(), two_pass, _stream())
+    assert st == 0, kai.current_direct_error()
+    torch.cuda.synchronize()
+    return act
+
+
+def used_bytes(buf, m, k, two_pass):
+    """The defined regions of an activation buffer (padding between passes is not written)."""
+    nb = k // 32
+    pass_bytes = (m * nb * 36 + 255) // 256 * 256
+    parts = [buf[:m * nb * 36]]
+    if two_pass:
+        parts.append(buf[pass_bytes:pass_bytes + m * nb * 36])
+    off = pass_bytes * (2 if two_pass else 1)
+    parts.append(buf[off:off + 4 * m])
+    return np.concatenate(parts)
+
+
+# ----------------------------------------------------------------- Q8_1 preparation
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,k", [(1, 2048), (3, 5120), (8, 17408), (16, 160), (33, 4096)])
+@pytest.mark.parametrize("two_pass", [0, 1])
+def test_prepare_bit_exact(kai, dtype, m, k, two_pass):
+    print(f"prepare dtype={dtype} m={m} k={k} two_pass={two_pass}", flush=True)
+    rng = np.random.default_rng(m * 7 + k)
+    x = (rng.standard_normal((m, k)) * rng.uniform(1e-2, 1e2, (m, 1))).astype(np.float32)
+    x_dev = to_dev(x).to(dtype)
+    act = gpu_prepare(kai, x_dev, two_pass).cpu().numpy()
+    if dtype == torch.bfloat16:
+        ref = O.prepare(x_dev.view(torch.int16).cpu().numpy().view(np.uint16), two_pass, dtype_code=1)
+    else:
+        ref = O.prepare(x_dev.cpu().numpy(), two_pass)
+    assert np.array_equal(used_bytes(act, m, k, two_pass), used_bytes(ref, m, k, two_pass))
+
+
+def test_prepare_special_rows_and_stride(kai):
+    print("prepare special rows", flush=True)
+    k = 256
+    x = np.random.default_rng(9).standard_normal((6, k + 64)).astype(np.float32)
+    x[0] = 0.0
+    x[1, :] = 0.0
+    x[1, 7] = 1e-41          # subnormal row maximum
+    x[2] *= 1e30             # huge row
+    x[3, :32] = 0.0          # a zero block inside a live row
+    x[4, 100] = 2.0 ** -126  # tiny but normal values
+    x[5] *= 1e-30
+    full = to_dev(x)
+    view = full[:, :k]       # row stride k + 64
+    act = gpu_prepare(kai, view).cpu().numpy()
+    ref = O.prepare(np.ascontiguousarray(x[:, :k]))
+    assert np.array_equal(used_bytes(act, 6, k, 0), used_bytes(ref, 6, k, 0))
+
+
+# ----------------------------------------------------------------- GEMV (kai_fused_mmvq)
+
+SHAPES = {O.Q8_0: (300, 1024), O.Q4_0: (300, 2048), O.Q4_K: (300, 1280), O.Q6_K: (300, 1536),
+          O.Q2_K: (300, 1024), O.IQ3_S: (300, 1280)}
+
+
+def gpu_mmvq(kai, qtype, w_dev, n, k, act, m, two_pass=0, bf16=False, stride=None, offset=0, out=None):
+    stride = stride or n
+    if out is None:
+        out = torch.full((m, stride), float("nan"), dtype=torch.bfloat16 if bf16 else torch.float32, device=DEV)
+    st = kai.kai_fused_mmvq(w_dev.data_ptr(), qtype, n, k, m, act.data_ptr(), two_pass,
+                            out.data_ptr() + offset * out.element_size(), 1 if bf16 else 0, stride, _stream())
+    assert st == 0, kai.current_direct_error()
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("qtype", O.WEIGHT_TYPES, ids=lambda t: O.NAMES[t])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("weights", ["random", "quantized"])
+def test_mmvq_parity_f32(kai, qtype, m, weights):
+    print(f"mmvq {O.NAMES[qtype]} m={m} {weights}", flush=True)
+    n, k = SHAPES[qtype]
+    rng = np.random.default_rng(100 * qtype + m)
+    if weights == "random":
+        w = O.random_blocks(qtype, n, k, rng)
+    else:
+        from kaillm_amd.formats import quantize
+        w = quantize(rng.normal(0, 0.02, (n, k)).astype(np.float32), qtype)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    act = gpu_prepare(kai, to_dev(x))
+    out = gpu_mmvq(kai, qtype, to_dev(w), n, k, act, m).cpu().numpy()
+    ref = O.mul_mat(qtype, w, k, O.prepare(x), m)
+    err = O.normwise_rel(out, ref)
+    print(f"  normwise rel err {err:.3e}")
+    assert err <= TOL_F32
+
+
+@pytest.mark.parametrize("qtype", O.WEIGHT_TYPES, ids=lambda t: O.NAMES[t])
+@pytest.mark.parametrize("m", [1, 4, 7])
+def test_mmvq_bf16_two_pass_and_merged_stride(kai, qtype, m):
+    print(f"mmvq bf16/two-pass/stride {O.NAMES[qtype]} m={m}", flush=True)
+    n, k = SHAPES[qtype]
+    rng = np.random.default_rng(7 * qtype + m)
+    w = O.random_blocks(qtype, n, k, rng)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w_dev = to_dev(w)
+    for two_pass in (0, 1):
+        act = gpu_prepare(kai, to_dev(x), two_pass)
+        ref = O.mul_mat(qtype, w, k, O.prepare(x, two_pass), m, two_pass)
+        # merged projection: this matrix owns columns [37, 37 + n) of a [m, n + 50] output
+        out = gpu_mmvq(kai, qtype, w_dev, n, k, act, m, two_pass, bf16=True, stride=n + 50, offset=37)
+        got = out.float().cpu().numpy()
+        assert np.isnan(got[:, :37]).all() and np.isnan(got[:, 37 + n:]).all()  # neighbours untouched
+        assert O.normwise_rel(got[:, 37:37 + n], ref) <= TOL_BF16
+        out32 = gpu_mmvq(kai, qtype, w_dev, n, k, act, m, two_pass).cpu().numpy()
+        assert O.normwise_rel(out32, ref) <= TOL_F32
+
+
+def test_two_pass_is_closer_to_float_activations(kai):
+    """Two passes carry ~16-bit activations, so the result moves toward W @ x."""
+    rng = np.random.default_rng(5)
+    n, k, m = 256, 2048, 2
+    w = O.random_blocks(O.Q8_0, n, k, rng)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    dense = x.astype(np.float64) @ O.dequantize(O.Q8_0, w, k).astype(np.float64).T
+    w_dev = to_dev(w)
+    errs = []
+    for two_pass in (0, 1):
+        out = gpu_mmvq(kai, O.Q8_0, w_dev, n, k, gpu_prepare(kai, to_dev(x), two_pass), m, two_pass)
+        errs.append(O.normwise_rel(out.cpu().numpy(), dense))
+    assert errs[1] < errs[0] / 10
+
+
+# ----------------------------------------------------------------- batched group (kai_fused_mmq_run)
+
+def gpu_mmq(kai, mats, x_dev, bf16=False, stride=0):
+    m, k = x_dev.shape
+    count = len(mats)
+    types = (ctypes.c_int * count)(*[t for t, _, _ in mats])
+    rows = (ctypes.c_int64 * count)(*[w.shape[0] for _, w, _ in mats])
+    ptrs = (ctypes.c_void_p * count)(*[wd.data_ptr() for _, _, wd in mats])
+    size = kai.kai_fused_mmq_workspace(0, types, rows, count, k, m, 0 if bf16 else 1)
+    assert size > 0, kai.current_direct_error()
+    total = sum(w.shape[0] for _, w, _ in mats)
+    ld = stride or total
+    out = torch.full((m, ld), float("nan"), dtype=torch.bfloat16 if bf16 else torch.float32, device=DEV)
+    scratch = torch.empty(size, dtype=torch.uint8, device=DEV)
+    code = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[x_dev.dtype]
+    st = kai.kai_fused_mmq_run(ptrs, types, rows, count, x_dev.data_ptr(), code, x_dev.stride(0), k, m,
+                               out.data_ptr(), 1 if bf16 else 0, stride, scratch.data_ptr(), size, 0, _stream())
+    assert st == 0, kai.current_direct_error()
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("m", [9, 16, 17, 40, 80])
+def test_mmq_group_parity(kai, m):
+    print(f"mmq group m={m}", flush=True)
+    rng = np.random.default_rng(m)
+    k = 1024
+    mats = []
+    for qtype, n in ((O.Q4_K, 96), (O.Q6_K, 64), (O.Q8_0, 36)):
+        w = O.random_blocks(qtype, n, k, rng)
+        mats.append((qtype, w, to_dev(w)))
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    act = O.prepare(x)
+    ref = np.concatenate([O.mul_mat(t, w, k, act, m) for t, w, _ in mats], axis=1)
+    out = gpu_mmq(kai, mats, to_dev(x)).cpu().numpy()
+    assert O.normwise_rel(out, ref) <= TOL_F32
+    outb = gpu_mmq(kai, mats, to_dev(x), bf16=True, stride=ref.shape[1] + 8).float().cpu().numpy()
+    assert O.normwise_rel(outb[:, :ref.shape[1]], ref) <= TOL_BF16
+    assert np.isnan(outb[:, ref.shape[1]:]).all()
+
+
+# ----------------------------------------------------------------- full BASELINE shapes
+
+FULL = [
+    ("C1 Q8_0 2048x2048", O.Q8_0, 2048, 2048, 1),
+    ("C2 Q4_0 gate/up", O.Q4_0, 16384, 2048, 8),
+    ("C2 Q4_0 down", O.Q4_0, 2048, 8192, 4),
+    ("C3 Q4_K gate/up", O.Q4_K, 34816, 5120, 1),
+    ("C3 Q4_K qkv", O.Q4_K, 7168, 5120, 16),
+    ("C3 Q6_K down", O.Q6_K, 5120, 17408, 2),
+    ("C3 Q6_K o_proj", O.Q6_K, 5120, 6144, 8),
+    ("C5 Q2_K gate/up", O.Q2_K, 34816, 5120, 1),
+    ("C5 IQ3_S down", O.IQ3_S, 5120, 17408, 16),
+]
+
+
+@pytest.mark.parametrize("name,qtype,n,k,m", FULL, ids=[f[0] for f in FULL])
+def test_full_size_configs(kai, name, qtype, n, k, m):
+    print(f"full {name} m={m}", flush=True)
+    rng = np.random.default_rng(n + k + m)
+    w = O.random_blocks(qtype, n, k, rng)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    x_dev = to_dev(x)
+    ref = O.mul_mat(qtype, w, k, O.prepare(x), m, threads=16)
+    if m <= 8:
+        out = gpu_mmvq(kai, qtype, to_dev(w), n, k, gpu_prepare(kai, x_dev), m)
+    else:
+        out = gpu_mmq(kai, [(qtype, w, to_dev(w))], x_dev)
+    err = O.normwise_rel(out.cpu().numpy(), ref)
+    print(f"  normwise rel err {err:.3e}")
+    assert err <= TOL_F32
+
+
+# ----------------------------------------------------------------- torch ops / apply()
+
+def test_fused_projection_torch_ops(kai):
+    from kaillm_amd.linear import GGUFLinearMethod, PackedGGUFLinear
+
+    rng = np.random.default_rng(77)
+    k = 1024
+    parts_np = [(O.Q4_K, O.random_blocks(O.Q4_K, 128, k, rng)), (O.Q6_K, O.random_blocks(O.Q6_K, 64, k, rng))]
+    layer = torch.nn.Module()
+    layer.gguf_compact = torch.nn.ModuleList(
+        [PackedGGUFLinear(to_dev(w), t, torch.bfloat16) for t, w in parts_np])
+    method = GGUFLinearMethod()
+    for m in (1, 3, 8, 12, 64):
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        x_dev = to_dev(x).to(torch.bfloat16)
+        act = O.prepare(x_dev.view(torch.int16).cpu().numpy().view(np.uint16), dtype_code=1)
+        ref = np.concatenate([O.mul_mat(t, w, k, act, m) for t, w in parts_np], axis=1)
+        bias = torch.randn(ref.shape[1], device=DEV, dtype=torch.bfloat16)
+        y = method.apply(layer, x_dev.reshape(1, m, k), bias)
+        assert y.shape == (1, m, ref.shape[1]) and y.dtype == torch.bfloat16
+        got = (y.float() - bias.float()).reshape(m, -1).cpu().numpy()
+        assert O.normwise_rel(got, ref) <= 2 * TOL_BF16
