@@ -15,6 +15,10 @@
 // read once into registers; wave64 reductions for the row maximum.
 #include "kai_launch.h"
 
+// Every rounding step must be the one the reference spells out. No floating-point
+// contraction in this file; see quantize_block for the fp16 conversion of d * sum.
+#pragma clang fp contract(off)
+
 namespace kai {
 
 constexpr int PREP_MAX_THREADS = 1024;  // K <= 32768
@@ -60,7 +64,12 @@ __device__ __forceinline__ float quantize_block(const float (&v)[32], block_q8_1
         isum += q[j];
     }
     const uint16_t hd = float_to_half_bits(d);
-    const uint16_t hs = float_to_half_bits(d * static_cast<float>(isum));
+    // half(d * sum) rounds the product to fp32 first, then to fp16. The backend would
+    // otherwise fold fmul + fptrunc into one v_fma_mixlo_f16, which rounds once and
+    // differs on exact fp16 ties; the empty asm makes the fp32 product opaque.
+    float prod = d * static_cast<float>(isum);
+    __asm__ volatile("" : "+v"(prod));
+    const uint16_t hs = float_to_half_bits(prod);
     uint32_t words[9];
     words[0] = static_cast<uint32_t>(hd) | (static_cast<uint32_t>(hs) << 16);
 #pragma unroll

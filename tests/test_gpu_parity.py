@@ -86,6 +86,23 @@ def test_prepare_special_rows_and_stride(kai):
     assert np.array_equal(used_bytes(act, 6, k, 0), used_bytes(ref, 6, k, 0))
 
 
+# 32 fp16 values (row maximum 166.4, so the row scale is 1/2) whose block sum term
+# d * sum(q) = 0.6550197 * 381 rounds in fp32 to exactly 249.5625, half-way between
+# two fp16 values: round-to-even gives 249.5; rounding the exact product once gives
+# 249.625. The reference rounds to fp32 first (kai_dual_mmvq.cuh:232).
+TIE_BLOCK_F16 = [22511, 51058, 21691, 20463, 18037, 20018, 19290, 22151, 21870, 18441, 48960, 54996,
+                 55402, 21306, 22255, 50731, 51473, 18990, 21410, 52474, 16546, 19595, 21490, 21887,
+                 20412, 20406, 53101, 19193, 55603, 53311, 18646, 20882]
+
+
+def test_prepare_fp16_sum_tie_rounds_via_fp32(kai):
+    x = np.array(TIE_BLOCK_F16, dtype=np.uint16).view(np.float16).reshape(1, 32)
+    act = gpu_prepare(kai, to_dev(x)).cpu().numpy()
+    ref = O.prepare(x)
+    assert ref[2:4].view(np.float16)[0] == np.float16(249.5)
+    assert np.array_equal(used_bytes(act, 1, 32, 0), used_bytes(ref, 1, 32, 0))
+
+
 # ----------------------------------------------------------------- GEMV (kai_fused_mmvq)
 
 SHAPES = {O.Q8_0: (300, 1024), O.Q4_0: (300, 2048), O.Q4_K: (300, 1280), O.Q6_K: (300, 1536),
