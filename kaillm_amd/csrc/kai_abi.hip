@@ -76,6 +76,25 @@ Group validate_group(const int *types, const int64_t *rows, int count, int64_t k
 
 }  // namespace
 
+namespace kai {
+
+int device_cu_count() {
+    static thread_local int cached_device = -1;
+    static thread_local int cached_count = 0;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) throw Error("No HIP device");
+    if (device != cached_device) {
+        int count = 0;
+        if (hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || count <= 0)
+            throw Error("Cannot query the compute unit count");
+        cached_device = device;
+        cached_count = count;
+    }
+    return cached_count;
+}
+
+}  // namespace kai
+
 extern "C" const char *current_direct_error(void) { return last_error.c_str(); }
 
 extern "C" int kai_fused_supported(int type, int64_t n, int64_t k, int64_t m) {

@@ -4,6 +4,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <algorithm>
 #include <stdexcept>
 #include <string>
 
@@ -17,6 +18,9 @@ struct Error : std::runtime_error {
 };
 
 constexpr int MMVQ_MAX_ROWS = 16;  // activation rows the GEMV kernel is built for
+
+// Compute units of the current device (cached per device).
+int device_cu_count();
 
 // Activation buffer layout: [pass1: m*(k/32) Q8_1 blocks, 256-aligned][pass2][inverse: m floats].
 inline size_t align256(size_t bytes) { return (bytes + 255) & ~size_t(255); }

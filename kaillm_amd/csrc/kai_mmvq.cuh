@@ -3,15 +3,19 @@
 //
 // Reference: kai_dual::mmvq_dual (vllm_gguf_plugin/native/kernels/kai_dual_mmvq.cuh:258-327)
 // and its launcher (:329-397). Design for gfx950 instead of warp32 CTAs:
-//   * one wave64 owns R consecutive output rows; its 64 lanes walk the row's units
-//     (kai_units.h) so each load instruction covers contiguous wire bytes;
-//   * every unit's activation slice (all m rows) is loaded once and reused for the
-//     R weight rows, which keeps L1/L2 traffic per weight byte low as m grows;
+//   * a wave64 works on 64/G rows at once, one group of G lanes per row (G = 8..64,
+//     chosen per shape so that short matrices with long rows still fill every CU);
+//     the lanes of a group walk the row's ~32-byte units (kai_units.h) in order, so
+//     each load instruction reads contiguous runs of G units of wire bytes;
+//   * a ring of DEPTH units per lane of wire bytes is kept in flight: unit t + DEPTH is
+//     requested before unit t is multiplied (DEPTH 2 keeps 5 waves per SIMD resident);
+//   * the activation (all m rows of Q8_1 blocks, byte for byte) is staged in LDS once
+//     per workgroup together with the exact code sums of every 16-value half, so the
+//     loop issues no vector-memory load other than the weight stream (vmcnt retires in
+//     issue order, so any other global load in the loop would wait for the whole ring);
 //   * integer dots with v_dot4_i32_i8, fp32 scale/accumulate per block;
-//   * per-row totals by a wave64 DPP/swizzle reduction, no LDS or barrier;
+//   * per-row totals by a DPP/swizzle reduction inside each lane group, no barrier;
 //   * merged-projection epilogue: x inverse[j], F32 or BF16, strided store.
-// Four independent waves per 256-thread workgroup. IQ3_S copies its 2 KiB grid
-// into LDS once per workgroup.
 #pragma once
 
 #include "kai_iq3s_grid.h"
@@ -23,8 +27,7 @@ namespace kai {
 // Each translation unit that instantiates the IQ3_S kernel owns a copy of the grid.
 static __device__ const uint32_t iq3s_grid_global[512] = {KAI_IQ3S_GRID_VALUES};
 
-constexpr int MMVQ_THREADS = 256;
-constexpr int MMVQ_WAVES = MMVQ_THREADS / WAVE;
+constexpr int MMVQ_LDS_BUDGET = 160 * 1024;
 
 template <int TYPE>
 __device__ __forceinline__ Unit<TYPE> make_unit(int sub, const uint32_t *grid) {
@@ -37,125 +40,223 @@ __device__ __forceinline__ void store_out(void *dst, bool bf16, int64_t index, f
     else static_cast<float *>(dst)[index] = v;
 }
 
-// Occupancy floor per activation-row count: enough waves in flight to cover HBM
-// latency, leaving registers for R x M accumulators and the prefetched units.
-template <int M> constexpr int mmvq_min_waves() { return M <= 2 ? 4 : 2; }
+// Sum over the G lanes of each lane group (lanes Gg..Gg+G-1); every lane gets its group's sum.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    v += dpp_f32<DPP_QUAD_1032>(v);
+    v += dpp_f32<DPP_QUAD_2301>(v);
+    v += dpp_f32<DPP_ROW_HALF_MIRROR>(v);
+    if constexpr (G >= 16) v += dpp_f32<DPP_ROW_MIRROR>(v);
+    if constexpr (G >= 32) v += __shfl_xor(v, 16, WAVE);
+    if constexpr (G >= 64) v += __shfl_xor(v, 32, WAVE);
+    return v;
+}
 
-template <int TYPE, int M, int R, bool TWO_PASS>
-__global__ __launch_bounds__(MMVQ_THREADS) __attribute__((amdgpu_waves_per_eu(mmvq_min_waves<M>(), 8)))
-void mmvq_kernel(
-    const uint8_t *__restrict__ weight, int64_t row_bytes, int nrows, int units_per_row,
-    const block_q8_1 *__restrict__ y1, const block_q8_1 *__restrict__ y2, int y_row_blocks,
-    const float *__restrict__ inverse, void *__restrict__ dst, int64_t stride_dst, int dst_bf16) {
+// LDS bytes of the staged activation: per pass and row, nb Q8_1 blocks (36 bytes) and
+// nb packed half sums (4 bytes).
+inline size_t mmvq_act_lds_bytes(int64_t m, int64_t k, bool two_pass) {
+    return size_t(two_pass ? 2 : 1) * size_t(m) * size_t(k / QK8_1) * 40;
+}
+
+template <int M> constexpr int mmvq_threads() { return M <= 4 ? 256 : 128; }
+
+template <int TYPE, int M, bool TWO_PASS, int DEPTH, int G>
+__global__ __launch_bounds__(mmvq_threads<M>())
+void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrows, int units_per_row,
+                 const block_q8_1 *__restrict__ y1, const block_q8_1 *__restrict__ y2, int y_row_blocks,
+                 const float *__restrict__ inverse, void *__restrict__ dst, int64_t stride_dst, int dst_bf16) {
     using U = Unit<TYPE>;
+    constexpr int THREADS = mmvq_threads<M>();
     constexpr int BYTES = block_bytes(TYPE);
+    constexpr int PASSES = TWO_PASS ? 2 : 1;
+    constexpr int ROWS = M * PASSES;  // activation rows staged
+    extern __shared__ __align__(16) uint8_t kai_mmvq_lds[];
     __shared__ uint32_t grid_lds[TYPE == IQ3_S ? 512 : 1];
+    __shared__ float inv_lds[M];
+
+    const int lane = threadIdx.x % WAVE;
+    const int gpos = lane % G;
+    const int row = (blockIdx.x * (THREADS / WAVE) + threadIdx.x / WAVE) * (WAVE / G) + lane / G;
+    const int nb = y_row_blocks;
+    const U unit = make_unit<TYPE>(gpos % U::PER_BLOCK, grid_lds);
+    const uint8_t *wrow = weight + static_cast<int64_t>(min(row, nrows - 1)) * row_bytes;
+    const int T = (units_per_row + G - 1) / G;
+
+    // Prime the ring first so the staging below overlaps the HBM latency.
+    typename U::W ring[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+        const int u = gpos + G * d;
+        if (d < T && u < units_per_row) unit.load_w(ring[d], wrow + static_cast<int64_t>(u / U::PER_BLOCK) * BYTES);
+    }
+
+    // Stage the IQ3_S grid, inverse[] and the activation: ROWS * nb blocks copied with
+    // 16-byte vectors, then the exact code sums of each block's two 16-value halves.
     if constexpr (TYPE == IQ3_S) {
-        for (int i = threadIdx.x; i < 512; i += MMVQ_THREADS) grid_lds[i] = iq3s_grid_global[i];
+        for (int i = threadIdx.x; i < 512; i += THREADS) grid_lds[i] = iq3s_grid_global[i];
+    }
+    if (threadIdx.x < M) inv_lds[threadIdx.x] = inverse[threadIdx.x];
+    uint8_t *act = kai_mmvq_lds;
+    uint32_t *sums = reinterpret_cast<uint32_t *>(kai_mmvq_lds + size_t(ROWS) * nb * 36);
+    {
+        const int pass_bytes = M * nb * 36;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const uint8_t *src = reinterpret_cast<const uint8_t *>(p ? y2 : y1);
+            uint8_t *dstl = act + p * pass_bytes;
+            const int vec = pass_bytes / 16;
+            for (int i = threadIdx.x; i < vec; i += THREADS) {
+                const uint4 v = load_unaligned<uint4>(src + 16 * i);  // 4-byte aligned runs
+                __builtin_memcpy(dstl + 16 * i, &v, 16);
+            }
+            for (int i = 4 * vec + threadIdx.x; i < pass_bytes / 4; i += THREADS)
+                reinterpret_cast<uint32_t *>(dstl)[i] = reinterpret_cast<const uint32_t *>(src)[i];
+        }
+        __syncthreads();
+        const uint4 ones = make_uint4(0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u);
+        for (int b = threadIdx.x; b < ROWS * nb; b += THREADS) {
+            const int slo = dot16(ones, load_unaligned<uint4>(act + 36 * b + 4));
+            const int shi = dot16(ones, load_unaligned<uint4>(act + 36 * b + 20));
+            sums[b] = (static_cast<uint32_t>(slo) & 0xffffu) | (static_cast<uint32_t>(shi) << 16);
+        }
         __syncthreads();
     }
-    const int wave = threadIdx.x / WAVE;
-    const int lane = threadIdx.x % WAVE;
-    const int row0 = (blockIdx.x * MMVQ_WAVES + wave) * R;
-    if (row0 >= nrows) return;
+    if (row - lane / G >= nrows) return;  // whole wave past the last row
 
-    const U unit = make_unit<TYPE>(lane % U::PER_BLOCK, grid_lds);
-    const uint8_t *rows[R];
+    float acc[M];
 #pragma unroll
-    for (int r = 0; r < R; ++r) rows[r] = weight + static_cast<int64_t>(min(row0 + r, nrows - 1)) * row_bytes;
+    for (int j = 0; j < M; ++j) acc[j] = 0.0f;
 
-    float acc[R][M];
+    for (int t0 = 0; t0 < T; t0 += DEPTH) {
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+        for (int d = 0; d < DEPTH; ++d) {
+            const int t = t0 + d;
+            if (t < T) {
+                const int u = gpos + G * t;
+                const bool live = u < units_per_row;
+                typename U::P w;
+                if (live) w = unit.prep(ring[d]);
+                const int un = u + G * DEPTH;
+                if (t + DEPTH < T && un < units_per_row)
+                    unit.load_w(ring[d], wrow + static_cast<int64_t>(un / U::PER_BLOCK) * BYTES);
+                if (live) {
+                    const int blk = u / U::PER_BLOCK;
 #pragma unroll
-        for (int j = 0; j < M; ++j) acc[r][j] = 0.0f;
-
-    // Software pipeline over the weight stream: the next unit's wire bytes are
-    // requested before the current unit is multiplied, so one unit per row of HBM
-    // reads stays in flight behind the arithmetic (activation slices hit L1/L2).
-    typename U::W next[R];
-    if (lane < units_per_row) {
+                    for (int j = 0; j < M; ++j) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) unit.load_w(next[r], rows[r] + static_cast<int64_t>(lane / U::PER_BLOCK) * BYTES);
-    }
-    for (int u = lane; u < units_per_row; u += WAVE) {
-        const int blk = u / U::PER_BLOCK;
-        typename U::P w[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) w[r] = unit.prep(next[r]);
-        if (u + WAVE < units_per_row) {
-            const int64_t nb = static_cast<int64_t>((u + WAVE) / U::PER_BLOCK) * BYTES;
-#pragma unroll
-            for (int r = 0; r < R; ++r) unit.load_w(next[r], rows[r] + nb);
-        }
-#pragma unroll
-        for (int j = 0; j < M; ++j) {
-            typename U::A a;
-            unit.load_a(a, y1 + static_cast<int64_t>(j) * y_row_blocks, blk);
-#pragma unroll
-            for (int r = 0; r < R; ++r) acc[r][j] += unit.dot(w[r], a);
-            if constexpr (TWO_PASS) {
-                typename U::A a2;
-                unit.load_a(a2, y2 + static_cast<int64_t>(j) * y_row_blocks, blk);
-#pragma unroll
-                for (int r = 0; r < R; ++r) acc[r][j] += unit.dot(w[r], a2);
+                        for (int p = 0; p < PASSES; ++p) {
+                            const int r = p * M + j;
+                            typename U::A a;
+                            unit.load_a(a, ActLds{act + size_t(r) * nb * 36, sums + size_t(r) * nb}, blk);
+                            acc[j] += unit.dot(w, a);
+                        }
+                    }
+                }
             }
         }
     }
 
-    // Every lane ends with every total; lane (r*M + j) stores item (r, j).
+    // Group totals; lane gpos of a group stores activation rows j = gpos, gpos + G, ...
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-#pragma unroll
-        for (int j = 0; j < M; ++j) {
-            const float total = wave_sum(acc[r][j]);
-            if (lane == (r * M + j) % WAVE && row0 + r < nrows) {
-                store_out(dst, dst_bf16 != 0, static_cast<int64_t>(j) * stride_dst + row0 + r, total * inverse[j]);
-            }
-        }
+    for (int j = 0; j < M; ++j) {
+        const float total = group_sum<G>(acc[j]);
+        if (gpos == j % G && row < nrows)
+            store_out(dst, dst_bf16 != 0, static_cast<int64_t>(j) * stride_dst + row, total * inv_lds[j]);
     }
 }
 
-// Rows per wave: more rows reuse each activation slice more often (fewer L1/L2
-// bytes per weight byte) at the cost of registers.
-template <int M> constexpr int rows_per_wave() { return M <= 2 ? 2 : M <= 8 ? 4 : 2; }
-
-template <int TYPE, int M>
-static void launch_m(const void *weight, int64_t n, int64_t k, const block_q8_1 *y1, const block_q8_1 *y2,
-                     const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
-    constexpr int R = rows_per_wave<M>();
+template <int TYPE, int M, bool TWO_PASS, int G>
+static void launch_variant(const uint8_t *w, int64_t n, int64_t k, const block_q8_1 *y1, const block_q8_1 *y2,
+                           const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
+    constexpr int THREADS = mmvq_threads<M>();
+    constexpr int DEPTH = 2;
     constexpr int QK = block_elems(TYPE);
     const int64_t blocks_per_row = k / QK;
     const int64_t row_bytes = blocks_per_row * block_bytes(TYPE);
     const int units = static_cast<int>(blocks_per_row * Unit<TYPE>::PER_BLOCK);
-    const int64_t rows_per_group = int64_t(MMVQ_WAVES) * R;
-    const dim3 grid(static_cast<unsigned>((n + rows_per_group - 1) / rows_per_group));
-    const auto *w = static_cast<const uint8_t *>(weight);
-    const int yrb = static_cast<int>(k / QK8_1);
-    if (y2) {
-        if constexpr (M <= 8) {
-            mmvq_kernel<TYPE, M, R, true><<<grid, MMVQ_THREADS, 0, stream>>>(
-                w, row_bytes, static_cast<int>(n), units, y1, y2, yrb, inverse, dst, stride_dst, dst_bf16 ? 1 : 0);
-        } else {
-            throw Error("Two-pass activations are supported for up to 8 rows");
-        }
-    } else {
-        mmvq_kernel<TYPE, M, R, false><<<grid, MMVQ_THREADS, 0, stream>>>(
-            w, row_bytes, static_cast<int>(n), units, y1, y2, yrb, inverse, dst, stride_dst, dst_bf16 ? 1 : 0);
+    const int64_t rows_per_block = (THREADS / WAVE) * (WAVE / G);
+    const size_t lds = mmvq_act_lds_bytes(M, k, TWO_PASS);
+    if (lds + (TYPE == IQ3_S ? 2048 : 0) + 64 > size_t(MMVQ_LDS_BUDGET))
+        throw Error("GEMV activation does not fit in LDS (m * k too large)");
+    auto kernel = mmvq_kernel<TYPE, M, TWO_PASS, DEPTH, G>;
+    static bool attribute_set = false;  // per instantiation; raises the dynamic LDS limit once
+    if (!attribute_set) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                MMVQ_LDS_BUDGET - 4096) != hipSuccess)
+            throw Error("Cannot raise the GEMV dynamic LDS limit");
+        attribute_set = true;
+    }
+    kernel<<<dim3(static_cast<unsigned>((n + rows_per_block - 1) / rows_per_block)), dim3(THREADS), lds, stream>>>(
+        w, row_bytes, static_cast<int>(n), units, y1, y2, static_cast<int>(k / QK8_1), inverse, dst, stride_dst,
+        dst_bf16 ? 1 : 0);
+}
+
+// Lanes per row: the smallest group that still yields about eight workgroups per CU
+// (short waves keep the tail of the launch short), widened only while a row keeps
+// more than 4 units per lane.
+template <int TYPE, int M>
+static int pick_group(int64_t n, int64_t k) {
+    const int64_t units = (k / block_elems(TYPE)) * Unit<TYPE>::PER_BLOCK;
+    const int64_t target_blocks = int64_t(device_cu_count()) * 8;
+    const int waves = mmvq_threads<M>() / WAVE;
+    int g = 8;
+    while (g < 64 && (n + (waves * (WAVE / g)) - 1) / (waves * (WAVE / g)) < target_blocks && units / g > 4) g *= 2;
+    return g;
+}
+
+template <int TYPE, int M, bool TWO_PASS>
+static void launch_group(const uint8_t *w, int64_t n, int64_t k, const block_q8_1 *y1, const block_q8_1 *y2,
+                         const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
+    switch (pick_group<TYPE, M>(n, k)) {
+        case 8: launch_variant<TYPE, M, TWO_PASS, 8>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream); break;
+        case 16: launch_variant<TYPE, M, TWO_PASS, 16>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream); break;
+        case 32: launch_variant<TYPE, M, TWO_PASS, 32>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream); break;
+        default: launch_variant<TYPE, M, TWO_PASS, 64>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream); break;
     }
 }
 
-// Per-type entry used by launch_mmvq; one translation unit per type keeps builds parallel.
+template <int TYPE, int M>
+static void launch_m(const void *weight, int64_t n, int64_t k, const block_q8_1 *y1, const block_q8_1 *y2,
+                     const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
+    const auto *w = static_cast<const uint8_t *>(weight);
+    if (y2) {
+        if constexpr (M <= 8) launch_group<TYPE, M, true>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream);
+        else throw Error("Two-pass activations are supported for up to 8 rows");
+    } else {
+        launch_group<TYPE, M, false>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream);
+    }
+}
+
 template <int TYPE>
-void launch_mmvq_type(const void *weight, int64_t n, int64_t k, int64_t m, const block_q8_1 *y1,
-                      const block_q8_1 *y2, const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst,
-                      hipStream_t stream) {
+static void launch_rows(const void *weight, int64_t n, int64_t k, int64_t m, const block_q8_1 *y1,
+                        const block_q8_1 *y2, const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst,
+                        hipStream_t stream) {
     switch (m) {
 #define KAI_M(MM) case MM: launch_m<TYPE, MM>(weight, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream); break;
         KAI_M(1) KAI_M(2) KAI_M(3) KAI_M(4) KAI_M(5) KAI_M(6) KAI_M(7) KAI_M(8)
         KAI_M(9) KAI_M(10) KAI_M(11) KAI_M(12) KAI_M(13) KAI_M(14) KAI_M(15) KAI_M(16)
 #undef KAI_M
         default: throw Error("GEMV supports 1..16 activation rows");
+    }
+}
+
+// Per-type entry used by launch_mmvq; one translation unit per type keeps builds parallel.
+// Activation rows are split into launches whose staged activation fits in LDS (each
+// launch streams the weights once).
+template <int TYPE>
+void launch_mmvq_type(const void *weight, int64_t n, int64_t k, int64_t m, const block_q8_1 *y1,
+                      const block_q8_1 *y2, const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst,
+                      hipStream_t stream) {
+    const int64_t per_row = int64_t(mmvq_act_lds_bytes(1, k, y2 != nullptr));
+    const int64_t fit = (MMVQ_LDS_BUDGET - 4096) / per_row;
+    if (fit < 1) throw Error("GEMV activation row does not fit in LDS");
+    const int64_t nb = k / QK8_1;
+    const size_t elem = dst_bf16 ? 2 : 4;
+    for (int64_t j0 = 0; j0 < m; j0 += fit) {
+        const int64_t mm = std::min(fit, m - j0);
+        launch_rows<TYPE>(weight, n, k, mm, y1 + j0 * nb, y2 ? y2 + j0 * nb : nullptr, inverse + j0,
+                          static_cast<char *>(dst) + size_t(j0) * size_t(stride_dst) * elem, dst_bf16, stride_dst,
+                          stream);
     }
 }
 
