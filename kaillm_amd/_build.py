@@ -21,6 +21,9 @@ ARCH = "gfx950"
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results straight into VGPRs: the MMQ epilogue scales every MFMA output on the
+    # VALU, and the AGPR form would add a v_accvgpr_read per element
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 CXX_FLAGS = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-pthread"]
 

@@ -166,11 +166,16 @@ extern "C" int kai_fused_mmq_run(const void *const *weights, const int *types, c
         const size_t elem = dst_bf16 ? 2 : 4;
         int64_t col = 0;
         for (int i = 0; i < count; ++i) {
-            for (int64_t j0 = 0; j0 < m; j0 += kai::MMVQ_MAX_ROWS) {
-                const int64_t mm = std::min<int64_t>(kai::MMVQ_MAX_ROWS, m - j0);
-                char *out = static_cast<char *>(dst) + (j0 * ld + col) * elem;
-                kai::launch_mmvq(types[i], weights[i], rows[i], k, mm, l.y1 + j0 * yrb, nullptr, l.inverse + j0, out,
-                                 dst_bf16 != 0, ld, s);
+            char *out = static_cast<char *>(dst) + col * elem;
+            if (k % 256 == 0) {
+                kai::launch_mmq(types[i], weights[i], rows[i], k, m, l.y1, l.inverse, out, dst_bf16 != 0, ld, s);
+            } else {
+                // k not a multiple of the 256-value MMQ step: GEMV launches of up to 16 rows
+                for (int64_t j0 = 0; j0 < m; j0 += kai::MMVQ_MAX_ROWS) {
+                    const int64_t mm = std::min<int64_t>(kai::MMVQ_MAX_ROWS, m - j0);
+                    kai::launch_mmvq(types[i], weights[i], rows[i], k, mm, l.y1 + j0 * yrb, nullptr, l.inverse + j0,
+                                     out + j0 * ld * elem, dst_bf16 != 0, ld, s);
+                }
             }
             col += rows[i];
         }

@@ -36,4 +36,8 @@ void launch_mmvq(int type, const void *weight, int64_t n, int64_t k, int64_t m, 
                  const block_q8_1 *y2, const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst,
                  hipStream_t stream);
 
+// Batched GEMM (int8 MFMA), m > 8 rows, k % 256 == 0: dst[j*stride_dst + r] as above.
+void launch_mmq(int type, const void *weight, int64_t n, int64_t k, int64_t m, const block_q8_1 *y,
+                const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream);
+
 }  // namespace kai

@@ -1,0 +1,548 @@
+// Batched GEMM for more than 8 activation rows (kernels 2 and 3): multi-sequence
+// decode, spec-verify (m = 16..80) and prefill (m = 512..2048), on int8 MFMA.
+//
+// Y[m, n] = inverse[m] * sum_b dot(W[n, b], q8[m, b]): the same exact per-block integer
+// dot products and fp32 scalings as the GEMV (reference: kai_fused_mmq_run,
+// vllm_gguf_plugin/native/kernels/current_ggml_direct.cu:1196-1265).
+//
+// Design for gfx950 (wave64, v_mfma_i32_16x16x32_i8):
+//   * each wave owns 16*TN weight rows and streams their wire bytes from HBM straight
+//     into registers (two K steps in flight); a lane holds, for its row (lane % 16) and
+//     octet (lane / 16), the 8 codes of every 32-value block that the MFMA B operand
+//     needs, so weights never pass through LDS and the wave needs no barrier for them;
+//   * the activation rows of the tile (MT = 16*TM) are staged once per K step into LDS
+//     by the whole workgroup (double-buffered, one barrier per step) in an MFMA layout:
+//     codes [block][row][32], scales d8 [block][row], and the activation factors of the
+//     min terms [term][row], so the A operand is one ds_read_b64 and the four row
+//     scales of a lane one ds_read_b128;
+//   * per 32-value block: one int8 MFMA gives the exact block dot of 16 rows x 16 weight
+//     rows, the fp32 epilogue multiplies by d8 * weight scale (three VALU operations
+//     per element, the bound of this kernel: the scales on both operands change every
+//     32 values, so the integer accumulation cannot run across blocks);
+//   * min/offset terms (Q4_0 8*s8, Q4_K dmin*m*sum, Q2_K per-16 mins) are small rank-8/16
+//     products per K step: they run on v_mfma_f32_16x16x4_f32 into the same
+//     accumulators instead of the VALU;
+//   * several waves of a workgroup may split K (KS) when there are too few weight rows
+//     to fill the chip; their partial sums are added in LDS in a fixed order.
+// Operand layouts (checked on gfx950): 16x16x32_i8: lane l holds A row l%16 and B
+// column l%16 for k = 8*(l/16) .. +8; 16x16x4_f32: A row l%16, B column l%16, k = l/16;
+// both: D column l%16, rows 4*(l/16) + i.
+#pragma once
+
+#include "kai_iq3s_grid.h"
+#include "kai_launch.h"
+#include "kai_units.h"
+
+namespace kai {
+
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+
+static __device__ const uint32_t mmq_iq3s_grid[512] = {KAI_IQ3S_GRID_VALUES};
+
+constexpr int MMQ_THREADS = 256;
+constexpr int MMQ_STEP = 256;  // values per K step (one superblock, or 8 blocks of 32)
+
+__device__ __forceinline__ uint64_t u64(uint2 v) { return uint64_t(v.x) | (uint64_t(v.y) << 32); }
+__device__ __forceinline__ uint32_t bits(uint32_t w, uint32_t shift, uint32_t width) {
+    return (w >> shift) & ((1u << width) - 1u);
+}
+
+// Weight side of the MMQ kernel, per format: what one lane loads for one K step of its
+// row (load), the int8 codes of its octet of block kb (codes), the scale of block kb
+// (scale: multiplies d8 * C), and the weight factors of the min terms (term: the B
+// operand of the fp32 MFMA for terms 4j .. 4j+3, the lane taking term 4j + oct).
+template <int TYPE> struct MmqW;
+
+// Q8_0: 8 blocks of 34 bytes per step. y += d8 * d * C. vecdotq.cuh:165-177.
+template <> struct MmqW<Q8_0> {
+    static constexpr int SB = 8 * 34, NTERM = 0;
+    static constexpr bool SPLIT16 = false;
+    struct Raw { uint2 q[8]; uint32_t d[8]; };
+    static __device__ void load(Raw &r, const uint8_t *p, int o) {
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            r.d[b] = load_unaligned<uint16_t>(p + 34 * b);
+            r.q[b] = load_unaligned<uint2>(p + 34 * b + 2 + 8 * o);
+        }
+    }
+    static __device__ uint64_t codes(const Raw &r, int b, int, const uint32_t *) { return u64(r.q[b]); }
+    static __device__ float scale(const Raw &r, int b) { return half_bits_to_float(r.d[b]); }
+    static __device__ float term(const Raw &, int, int) { return 0.0f; }
+};
+
+// Q4_0: 8 blocks of 18 bytes; value v < 16 is the low nibble of qs[v], v >= 16 the high
+// nibble of qs[v - 16]. y += d * (d8 * C - 8 * s8), s8 the stored fp16 d8*sum(q8).
+// vecdotq.cuh:46-66.
+template <> struct MmqW<Q4_0> {
+    static constexpr int SB = 8 * 18, NTERM = 8;
+    static constexpr bool SPLIT16 = false;
+    struct Raw { uint2 q[8]; uint32_t d[8]; };
+    static __device__ void load(Raw &r, const uint8_t *p, int o) {
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            r.d[b] = load_unaligned<uint16_t>(p + 18 * b);
+            r.q[b] = load_unaligned<uint2>(p + 18 * b + 2 + 8 * (o & 1));
+        }
+    }
+    static __device__ uint64_t codes(const Raw &r, int b, int o, const uint32_t *) {
+        return (u64(r.q[b]) >> (4 * (o >> 1))) & 0x0f0f0f0f0f0f0f0full;
+    }
+    static __device__ float scale(const Raw &r, int b) { return half_bits_to_float(r.d[b]); }
+    static __device__ float term(const Raw &r, int j, int o) {  // block 4j + o: -8 d
+        const uint32_t d = o == 0 ? r.d[4 * j] : o == 1 ? r.d[4 * j + 1] : o == 2 ? r.d[4 * j + 2] : r.d[4 * j + 3];
+        return -8.0f * half_bits_to_float(d);
+    }
+};
+
+// Q4_K superblock: d, dmin (fp16), 12 bytes of 6-bit scales/mins, qs[128]. Chunk c holds
+// blocks 2c (low nibbles) and 2c+1 (high nibbles); octet o of both is qs[32c + 8o, +8).
+// y += d8 * d * sc * C - dmin * m * (d8 * sum(q8)). vecdotq.cuh:328-351; scale packing
+// gguf-py quants.py:480-502.
+template <> struct MmqW<Q4_K> {
+    static constexpr int SB = 144, NTERM = 8;
+    static constexpr bool SPLIT16 = false;
+    struct Raw { uint4 hdr; uint2 q[4]; };
+    static __device__ void load(Raw &r, const uint8_t *p, int o) {
+        r.hdr = load_unaligned<uint4>(p);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) r.q[c] = load_unaligned<uint2>(p + 16 + 32 * c + 8 * o);
+    }
+    static __device__ uint64_t codes(const Raw &r, int b, int, const uint32_t *) {
+        const uint64_t q = u64(r.q[b / 2]);
+        return ((b & 1) ? q >> 4 : q) & 0x0f0f0f0f0f0f0f0full;
+    }
+    static __device__ float scale(const Raw &r, int b) {
+        const float d = half_bits_to_float(r.hdr.x & 0xffffu);
+        const uint32_t sc = b < 4 ? bits(r.hdr.y, 8 * b, 6)
+                                  : bits(r.hdr.w, 8 * (b - 4), 4) | (bits(r.hdr.y, 8 * (b - 4) + 6, 2) << 4);
+        return d * static_cast<float>(sc);
+    }
+    static __device__ float term(const Raw &r, int j, int o) {  // block 4j + o: -dmin * m
+        const float dmin = half_bits_to_float(r.hdr.x >> 16);
+        const uint32_t mn = j == 0 ? bits(r.hdr.z, 8 * o, 6)
+                                   : bits(r.hdr.w, 8 * o + 4, 4) | (bits(r.hdr.z, 8 * o + 6, 2) << 4);
+        return -dmin * static_cast<float>(mn);
+    }
+};
+
+// Q6_K superblock: ql[128], qh[64], int8 scales[16], d. Block kb = 4h + s, value v:
+// ql[64h + 32(s&1) + v] nibble s>>1, qh[32h + v] bits 2s; code q - 32 with one int8
+// scale per 16 values, so two MFMAs per block (the other half's codes zeroed) and the
+// two scales combined in 24-bit integer arithmetic. vecdotq.cuh:447-465; layout
+// gguf-py quants.py:553-573.
+template <> struct MmqW<Q6_K> {
+    static constexpr int SB = 210, NTERM = 0;
+    static constexpr bool SPLIT16 = true;
+    struct Raw { uint2 ql[4]; uint2 qh[2]; uint4 sc; uint32_t d; };
+    static __device__ void load(Raw &r, const uint8_t *p, int o) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.ql[i] = load_unaligned<uint2>(p + 64 * (i / 2) + 32 * (i % 2) + 8 * o);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) r.qh[h] = load_unaligned<uint2>(p + 128 + 32 * h + 8 * o);
+        r.sc = load_unaligned<uint4>(p + 192);
+        r.d = load_unaligned<uint16_t>(p + 208);
+    }
+    static __device__ uint64_t codes(const Raw &r, int b, int, const uint32_t *) {
+        const int h = b / 4, s = b % 4;
+        const uint64_t ql = u64(r.ql[2 * h + (s & 1)]), qh = u64(r.qh[h]);
+        const uint64_t c = ((ql >> (4 * (s >> 1))) & 0x0f0f0f0f0f0f0f0full) | (((qh >> (2 * s)) & 0x0303030303030303ull) << 4);
+        // c - 32 per byte: flip bit 5 (6-bit two's complement), then sign-extend bit 5
+        const uint64_t t = c ^ 0x2020202020202020ull;
+        const uint64_t sign = t & 0x2020202020202020ull;
+        return t | (sign << 1) | (sign << 2);
+    }
+    static __device__ int iscale(const Raw &r, int g) {  // int8 scale of 16-value group g
+        const uint32_t w = g < 4 ? r.sc.x : g < 8 ? r.sc.y : g < 12 ? r.sc.z : r.sc.w;
+        return static_cast<int8_t>(bits(w, 8 * (g % 4), 8));
+    }
+    static __device__ float scale(const Raw &r, int) { return half_bits_to_float(r.d); }
+    static __device__ float term(const Raw &, int, int) { return 0.0f; }
+};
+
+// Q2_K superblock: scales[16] (low nibble scale, high nibble min, per 16 values),
+// qs[64], d, dmin. Block kb = 4h + s: code (qs[32h + v] >> 2s) & 3, multiplied by its
+// 4-bit scale (<= 45, no int8 overflow) so one MFMA covers both 16-value groups;
+// y += d8 * d * C' - dmin * (m_lo * d8 S_lo + m_hi * d8 S_hi). vecdotq.cuh:204-230;
+// layout gguf-py quants.py:407-429.
+template <> struct MmqW<Q2_K> {
+    static constexpr int SB = 84, NTERM = 16;
+    static constexpr bool SPLIT16 = false;
+    struct Raw { uint4 sc; uint2 q[2]; uint32_t dm; };
+    static __device__ void load(Raw &r, const uint8_t *p, int o) {
+        r.sc = load_unaligned<uint4>(p);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) r.q[h] = load_unaligned<uint2>(p + 16 + 32 * h + 8 * o);
+        r.dm = load_unaligned<uint32_t>(p + 80);
+    }
+    static __device__ uint32_t word(const Raw &r, int i) { return i == 0 ? r.sc.x : i == 1 ? r.sc.y : i == 2 ? r.sc.z : r.sc.w; }
+    static __device__ uint64_t codes(const Raw &r, int b, int o, const uint32_t *) {
+        const int h = b / 4, s = b % 4;
+        const uint64_t q = (u64(r.q[h]) >> (2 * s)) & 0x0303030303030303ull;
+        // scale byte 2b + (o >> 1) lies in word b / 2
+        const uint32_t sc = bits(word(r, b / 2), 8 * (2 * (b & 1) + (o >> 1)), 4);
+        return q * sc;
+    }
+    static __device__ float scale(const Raw &r, int) { return half_bits_to_float(r.dm & 0xffffu); }
+    static __device__ float term(const Raw &r, int j, int o) {  // 16-value group 4j + o: -dmin * m
+        return -half_bits_to_float(r.dm >> 16) * static_cast<float>(bits(word(r, j), 8 * o + 4, 4));
+    }
+};
+
+// IQ3_S superblock: d, qs[64] (8-bit grid index low bits), qh[8], signs[32], scales[4].
+// Block kb, octet o: grid entries qs[8kb + 2o + i] | bit (2o + i) of qh[kb] << 8, signs
+// byte 4kb + o. y += d8 * d * (1 + 2 sc) * C. vecdotq.cuh:1649-1672; layout gguf-py
+// quants.py:1097-1125.
+template <> struct MmqW<IQ3_S> {
+    static constexpr int SB = 110, NTERM = 0;
+    static constexpr bool SPLIT16 = false;
+    struct Raw { uint32_t qs[8]; uint32_t sg[8]; uint2 qh; uint32_t sc; uint32_t d; };
+    static __device__ void load(Raw &r, const uint8_t *p, int o) {
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            r.qs[b] = load_unaligned<uint16_t>(p + 2 + 8 * b + 2 * o);
+            r.sg[b] = p[74 + 4 * b + o];
+        }
+        r.qh = load_unaligned<uint2>(p + 66);
+        r.sc = load_unaligned<uint32_t>(p + 106);
+        r.d = load_unaligned<uint16_t>(p);
+    }
+    static __device__ uint64_t codes(const Raw &r, int b, int o, const uint32_t *grid) {
+        const uint32_t qh = bits(b < 4 ? r.qh.x : r.qh.y, 8 * (b % 4), 8) >> (2 * o);
+        const uint32_t i0 = (r.qs[b] & 0xffu) | ((qh & 1u) << 8);
+        const uint32_t i1 = (r.qs[b] >> 8) | ((qh & 2u) << 7);
+        return uint64_t(Unit<IQ3_S>::signed_levels(grid[i0], r.sg[b] & 0x0fu)) |
+               (uint64_t(Unit<IQ3_S>::signed_levels(grid[i1], r.sg[b] >> 4)) << 32);
+    }
+    static __device__ float scale(const Raw &r, int b) {
+        return half_bits_to_float(r.d) * static_cast<float>(1 + 2 * static_cast<int>(bits(r.sc, 4 * b, 4)));
+    }
+    static __device__ float term(const Raw &, int, int) { return 0.0f; }
+};
+
+// Activation factors of the min terms for block kb of one row, from its Q8_1 block.
+template <int TYPE>
+__device__ __forceinline__ void act_terms(const uint4 q0, const uint4 q1, uint32_t ds, float d8, float *t) {
+    if constexpr (TYPE == Q4_0) {
+        t[0] = half_bits_to_float(ds >> 16);  // stored s8
+    } else if constexpr (TYPE == Q4_K || TYPE == Q2_K) {
+        const uint4 ones = make_uint4(0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u);
+        const int lo = dot16(ones, q0), hi = dot16(ones, q1);
+        if constexpr (TYPE == Q4_K) {
+            t[0] = d8 * static_cast<float>(lo + hi);
+        } else {
+            t[0] = d8 * static_cast<float>(lo);
+            t[1] = d8 * static_cast<float>(hi);
+        }
+    }
+}
+
+template <int TYPE, int TM>
+constexpr int mmq_buf_bytes() {  // one K step of MT activation rows in LDS
+    return 16 * TM * (8 * 32 + 8 * 4 + MmqW<TYPE>::NTERM * 4);
+}
+
+template <int TYPE, int TM, int TN, int KS>
+constexpr size_t mmq_lds_bytes() {
+    const size_t act = size_t(2) * KS * mmq_buf_bytes<TYPE, TM>();
+    const size_t red = KS > 1 ? size_t(KS - 1) * (4 / KS) * WAVE * TM * TN * 4 * sizeof(float) : 0;
+    return act > red ? act : red;
+}
+
+template <int TYPE, int TM, int TN, int KS, int DEPTH>
+__global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
+    const uint8_t *__restrict__ weight, int64_t row_bytes, int n, int k, const block_q8_1 *__restrict__ y,
+    int m, const float *__restrict__ inverse, void *__restrict__ dst, int64_t stride_dst, int dst_bf16) {
+    using W = MmqW<TYPE>;
+    constexpr int MT = 16 * TM, RG = 4 / KS, NT = W::NTERM;
+    constexpr int BUF = mmq_buf_bytes<TYPE, TM>();
+    constexpr int D8_OFF = MT * 8 * 32, TA_OFF = D8_OFF + MT * 8 * 4;
+    constexpr int PAIRS = KS * MT * 8;  // (k-group, row, block) activation blocks per iteration
+    constexpr int PP = (PAIRS + MMQ_THREADS - 1) / MMQ_THREADS;
+    extern __shared__ __align__(16) uint8_t kai_mmq_lds[];
+    __shared__ uint32_t grid_lds[TYPE == IQ3_S ? 512 : 1];
+
+    const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
+    const int rg = wave % RG, kg = wave / RG;
+    const int col = lane % 16, oct = lane / 16;
+    const int nb = k / QK8_1, steps = k / MMQ_STEP;
+    const int iters = (steps + KS - 1) / KS;
+    const int m0 = blockIdx.y * MT;
+    const int nrow0 = blockIdx.x * (16 * TN * RG) + rg * 16 * TN;
+    if constexpr (TYPE == IQ3_S) {
+        for (int i = tid; i < 512; i += MMQ_THREADS) grid_lds[i] = mmq_iq3s_grid[i];
+    }
+    const uint8_t *wrow[TN];
+#pragma unroll
+    for (int t = 0; t < TN; ++t) wrow[t] = weight + int64_t(min(nrow0 + 16 * t + col, n - 1)) * row_bytes;
+
+    // ---- activation staging: global Q8_1 blocks -> registers -> LDS (MFMA layout)
+    uint4 aq0[PP], aq1[PP];
+    uint32_t ads[PP];
+    auto aload = [&](int it) {
+#pragma unroll
+        for (int p = 0; p < PP; ++p) {
+            const int idx = tid + p * MMQ_THREADS;
+            const int r = idx % MT, b = (idx / MT) % 8, g = idx / (MT * 8);
+            const int s = it * KS + g, row = m0 + r;
+            aq0[p] = aq1[p] = make_uint4(0, 0, 0, 0);
+            ads[p] = 0;
+            if (idx < PAIRS && s < steps && row < m) {
+                const uint8_t *src = reinterpret_cast<const uint8_t *>(y + int64_t(row) * nb + 8 * s + b);
+                ads[p] = load_unaligned<uint32_t>(src);
+                aq0[p] = load_unaligned<uint4>(src + 4);
+                aq1[p] = load_unaligned<uint4>(src + 20);
+            }
+        }
+    };
+    // Codes of row r, block b: 32 bytes at (b*MT + r)*32 with the four 8-byte octets
+    // placed at position oct ^ ((r >> 2) & 3), so that the A-operand reads of a wave
+    // (16 rows x 4 octets) hit distinct banks.
+    auto astore = [&](int buf) {
+#pragma unroll
+        for (int p = 0; p < PP; ++p) {
+            const int idx = tid + p * MMQ_THREADS;
+            if (idx < PAIRS) {
+                const int r = idx % MT, b = (idx / MT) % 8, g = idx / (MT * 8);
+                const int sw = (r >> 2) & 3;
+                uint8_t *base = kai_mmq_lds + (buf * KS + g) * BUF;
+                uint4 *q = reinterpret_cast<uint4 *>(base + (b * MT + r) * 32);
+                const uint4 h0 = sw & 1 ? make_uint4(aq0[p].z, aq0[p].w, aq0[p].x, aq0[p].y) : aq0[p];
+                const uint4 h1 = sw & 1 ? make_uint4(aq1[p].z, aq1[p].w, aq1[p].x, aq1[p].y) : aq1[p];
+                q[sw >> 1] = h0;
+                q[(sw >> 1) ^ 1] = h1;
+                const float d8 = half_bits_to_float(ads[p] & 0xffffu);
+                reinterpret_cast<float *>(base + D8_OFF)[b * MT + r] = d8;
+                if constexpr (NT > 0) {
+                    float t[2];
+                    act_terms<TYPE>(aq0[p], aq1[p], ads[p], d8, t);
+                    float *ta = reinterpret_cast<float *>(base + TA_OFF);
+                    if constexpr (NT == 8) {
+                        ta[b * MT + r] = t[0];
+                    } else {
+                        ta[(2 * b) * MT + r] = t[0];
+                        ta[(2 * b + 1) * MT + r] = t[1];
+                    }
+                }
+            }
+        }
+    };
+
+    // ---- weights: DEPTH K steps in flight per wave
+    typename W::Raw wr[DEPTH][TN];
+    auto wload = [&](typename W::Raw (&w)[TN], int it) {
+        const int s = it * KS + kg;
+        if (s < steps) {
+#pragma unroll
+            for (int t = 0; t < TN; ++t) W::load(w[t], wrow[t] + int64_t(s) * W::SB, oct);
+        }
+    };
+
+    v4f_t acc[TM][TN];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int t = 0; t < TN; ++t) acc[a][t] = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto compute = [&](const typename W::Raw (&w)[TN], int buf, int it) {
+        if (it * KS + kg >= steps) return;  // wave-uniform
+        const uint8_t *base = kai_mmq_lds + (buf * KS + kg) * BUF;
+        const float *d8s = reinterpret_cast<const float *>(base + D8_OFF);
+        const v4i_t zero = {0, 0, 0, 0};
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            uint64_t bq[TN], bq2[TN];
+            float sa[TN];
+            int sl[TN], sh[TN];
+#pragma unroll
+            for (int t = 0; t < TN; ++t) {
+                const uint64_t c = W::codes(w[t], b, oct, grid_lds);
+                if constexpr (W::SPLIT16) {
+                    bq[t] = oct < 2 ? c : 0ull;
+                    bq2[t] = oct < 2 ? 0ull : c;
+                    sl[t] = MmqW<Q6_K>::iscale(w[t], 2 * b);
+                    sh[t] = MmqW<Q6_K>::iscale(w[t], 2 * b + 1);
+                } else {
+                    bq[t] = c;
+                }
+                sa[t] = W::scale(w[t], b);
+            }
+#pragma unroll
+            for (int a = 0; a < TM; ++a) {
+                const long aq = *reinterpret_cast<const long *>(base + (b * MT + 16 * a + col) * 32 + 8 * (oct ^ ((col >> 2) & 3)));
+                const float4 dv = *reinterpret_cast<const float4 *>(d8s + b * MT + 16 * a + 4 * oct);
+                const float d8[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+                for (int t = 0; t < TN; ++t) {
+                    const v4i_t c = __builtin_amdgcn_mfma_i32_16x16x32_i8(aq, static_cast<long>(bq[t]), zero, 0, 0, 0);
+                    if constexpr (W::SPLIT16) {
+                        const v4i_t c2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(aq, static_cast<long>(bq2[t]), zero, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int x = __mul24(sl[t], c[i]) + __mul24(sh[t], c2[i]);
+                            acc[a][t][i] = fmaf(d8[i] * sa[t], static_cast<float>(x), acc[a][t][i]);
+                        }
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[a][t][i] = fmaf(d8[i] * sa[t], static_cast<float>(c[i]), acc[a][t][i]);
+                    }
+                }
+            }
+        }
+        if constexpr (NT > 0) {
+            const float *ta = reinterpret_cast<const float *>(base + TA_OFF);
+#pragma unroll
+            for (int j = 0; j < NT / 4; ++j) {
+                float bt[TN];
+#pragma unroll
+                for (int t = 0; t < TN; ++t) bt[t] = W::term(w[t], j, oct);
+#pragma unroll
+                for (int a = 0; a < TM; ++a) {
+                    const float at = ta[(4 * j + oct) * MT + 16 * a + col];
+#pragma unroll
+                    for (int t = 0; t < TN; ++t) acc[a][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(at, bt[t], acc[a][t], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // ---- pipeline. Per iteration: compute step it from LDS buffer it & 1, stage the
+    // activation of step it+1 (loaded one iteration earlier) into the other buffer, load
+    // the activation of step it+2, then the weights of step it+DEPTH. Vector loads retire
+    // in order, so the wait for the activation of it+1 only covers weights that were
+    // already due; the far-ahead weight loads stay in flight across the barrier.
+    aload(0);
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) wload(wr[d], d);
+    astore(0);
+    aload(1);
+    __syncthreads();
+    for (int it0 = 0; it0 < iters; it0 += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            const int it = it0 + d;
+            if (it >= iters) break;
+            compute(wr[d], it & 1, it);
+            astore((it + 1) & 1);
+            aload(it + 2);
+            wload(wr[d], it + DEPTH);
+            __syncthreads();
+        }
+    }
+
+    // ---- K-split partial sums: k-groups 1.. write, k-group 0 adds in order
+    if constexpr (KS > 1) {
+        float *red = reinterpret_cast<float *>(kai_mmq_lds);
+        constexpr int PER = TM * TN * 4;
+        if (kg > 0) {
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+#pragma unroll
+                for (int t = 0; t < TN; ++t)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        red[(((kg - 1) * RG + rg) * PER + (a * TN + t) * 4 + i) * WAVE + lane] = acc[a][t][i];
+        }
+        __syncthreads();
+        if (kg == 0) {
+#pragma unroll
+            for (int g = 1; g < KS; ++g)
+#pragma unroll
+                for (int a = 0; a < TM; ++a)
+#pragma unroll
+                    for (int t = 0; t < TN; ++t)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            acc[a][t][i] += red[(((g - 1) * RG + rg) * PER + (a * TN + t) * 4 + i) * WAVE + lane];
+        }
+    }
+    if (kg != 0) return;
+
+    // ---- epilogue: x inverse[m], F32 or BF16, strided store
+#pragma unroll
+    for (int a = 0; a < TM; ++a) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = m0 + 16 * a + 4 * oct + i;
+            if (row >= m) continue;
+            const float inv = inverse[row];
+#pragma unroll
+            for (int t = 0; t < TN; ++t) {
+                const int c = nrow0 + 16 * t + col;
+                if (c < n) {
+                    const int64_t idx = int64_t(row) * stride_dst + c;
+                    if (dst_bf16) static_cast<uint16_t *>(dst)[idx] = float_to_bf16_bits(acc[a][t][i] * inv);
+                    else static_cast<float *>(dst)[idx] = acc[a][t][i] * inv;
+                }
+            }
+        }
+    }
+}
+
+template <int TYPE, int TM, int TN, int KS>
+static void launch_mmq_tile(const void *weight, int64_t n, int64_t k, const block_q8_1 *y, int64_t m,
+                            const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
+    constexpr int MT = 16 * TM, ROWS = 16 * TN * (4 / KS);
+    const int64_t row_bytes = (k / block_elems(TYPE)) * block_bytes(TYPE);
+    const size_t lds = mmq_lds_bytes<TYPE, TM, TN, KS>();
+    // weight steps in flight: deeper when the per-step work is short
+    constexpr int DEPTH = TM <= 2 ? 4 : 2;
+    auto kernel = mmq_kernel<TYPE, TM, TN, KS, DEPTH>;
+    static bool attribute_set = false;
+    if (!attribute_set) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(lds)) != hipSuccess)
+            throw Error("Cannot raise the MMQ dynamic LDS limit");
+        attribute_set = true;
+    }
+    const dim3 grid(static_cast<unsigned>((n + ROWS - 1) / ROWS), static_cast<unsigned>((m + MT - 1) / MT));
+    kernel<<<grid, MMQ_THREADS, lds, stream>>>(static_cast<const uint8_t *>(weight), row_bytes, static_cast<int>(n),
+                                               static_cast<int>(k), y, static_cast<int>(m), inverse, dst, stride_dst,
+                                               dst_bf16 ? 1 : 0);
+}
+
+// Tile choice. Activation tile MT = 16*TM rows: all rows up to 80 (weights streamed
+// once), 64-row tiles beyond (weights re-read per tile, from the last-level cache when
+// the tiles of one weight range run together). Weight rows per workgroup: 16*TN per
+// wave, with KS waves splitting K. The first choice that fills the chip with at least
+// two workgroups per CU wins, trying the full activation tile first; LDS per workgroup
+// stays within 80 KiB so that two fit on a CU.
+constexpr bool mmq_allowed(int tm, int ks) { return ks == 1 || (ks == 2 && tm <= 3) || (ks == 4 && tm == 1); }
+
+template <int TYPE>
+void launch_mmq_type(const void *weight, int64_t n, int64_t k, int64_t m, const block_q8_1 *y, const float *inverse,
+                     void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
+    if (k % MMQ_STEP) throw Error("MMQ needs k to be a multiple of 256");
+    static constexpr int CFG[5][2] = {{2, 1}, {1, 1}, {2, 2}, {1, 2}, {1, 4}};
+    // Q4_0 keeps 24 registers of wire bytes per row tile and K step: one tile per wave
+    constexpr bool wide = TYPE != Q4_0;
+    const int64_t want = 2 * int64_t(device_cu_count());
+    int tm = 1, tn = 1, ks = 4;
+    bool found = false;
+    for (int t = m > 80 ? 4 : static_cast<int>((m + 15) / 16); t >= 1 && !found; --t) {
+        for (const auto &c : CFG) {
+            if (!mmq_allowed(t, c[1]) || (c[0] == 2 && !wide)) continue;
+            const int64_t rows = 16 * c[0] * (4 / c[1]);
+            if ((n + rows - 1) / rows * ((m + 16 * t - 1) / (16 * t)) >= want) {
+                tm = t, tn = c[0], ks = c[1], found = true;
+                break;
+            }
+        }
+    }
+    const int key = tm * 100 + tn * 10 + ks;
+    switch (key) {
+#define KAI_C(TM, TN, KS) \
+    case TM * 100 + TN * 10 + KS: \
+        if constexpr (TN == 1 || wide) \
+            launch_mmq_tile<TYPE, TM, TN, KS>(weight, n, k, y, m, inverse, dst, dst_bf16, stride_dst, stream); \
+        break;
+        KAI_C(1, 2, 1) KAI_C(1, 1, 1) KAI_C(1, 2, 2) KAI_C(1, 1, 2) KAI_C(1, 1, 4)
+        KAI_C(2, 2, 1) KAI_C(2, 1, 1) KAI_C(2, 2, 2) KAI_C(2, 1, 2)
+        KAI_C(3, 2, 1) KAI_C(3, 1, 1) KAI_C(3, 2, 2) KAI_C(3, 1, 2)
+        KAI_C(4, 2, 1) KAI_C(4, 1, 1) KAI_C(5, 2, 1) KAI_C(5, 1, 1)
+#undef KAI_C
+        default: throw Error("MMQ tile selection failed");
+    }
+}
+
+}  // namespace kai

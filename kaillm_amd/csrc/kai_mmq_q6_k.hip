@@ -1,0 +1,7 @@
+// MMQ instantiations for Q6_K (kernel template in kai_mmq.cuh).
+#include "kai_mmq.cuh"
+
+namespace kai {
+template void launch_mmq_type<Q6_K>(const void *, int64_t, int64_t, int64_t, const block_q8_1 *, const float *, void *,
+                                  bool, int64_t, hipStream_t);
+}  // namespace kai

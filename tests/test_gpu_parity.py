@@ -218,6 +218,40 @@ def test_mmq_group_parity(kai, m):
     assert np.isnan(outb[:, ref.shape[1]:]).all()
 
 
+ALL_TYPES = [O.Q8_0, O.Q4_0, O.Q4_K, O.Q6_K, O.Q2_K, O.IQ3_S]
+
+
+@pytest.mark.parametrize("qtype", ALL_TYPES)
+@pytest.mark.parametrize("m,k,n", [(9, 768, 200), (24, 512, 64), (130, 256, 136), (300, 768, 72),
+                                   (20, 1056, 96)])
+def test_mmq_each_type(kai, qtype, m, k, n):
+    """Every format through the batched path: partial weight tiles (n % 128), several
+    activation tiles (m > 128), one K step (k = 256), and k % 256 != 0 (row-block path)."""
+    if k % O.BLOCK[qtype][0]:
+        pytest.skip("k not a multiple of this format's block")
+    print(f"mmq type={qtype} m={m} k={k} n={n}", flush=True)
+    rng = np.random.default_rng(qtype * 1000 + m + k)
+    w = O.random_blocks(qtype, n, k, rng)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    ref = O.mul_mat(qtype, w, k, O.prepare(x), m)
+    out = gpu_mmq(kai, [(qtype, w, to_dev(w))], to_dev(x)).cpu().numpy()
+    assert O.normwise_rel(out, ref) <= TOL_F32
+
+
+@pytest.mark.parametrize("qtype", [O.Q4_K, O.Q6_K, O.IQ3_S])
+def test_mmq_prefill_shape(kai, qtype):
+    """A prefill-sized call (m = 512) on a full-width weight, bf16 activations."""
+    m, n, k = 512, 1024, 2048
+    print(f"mmq prefill type={qtype} m={m} n={n} k={k}", flush=True)
+    rng = np.random.default_rng(qtype + 5)
+    w = O.random_blocks(qtype, n, k, rng)
+    x_dev = to_dev(rng.standard_normal((m, k)).astype(np.float32)).to(torch.bfloat16)
+    act = O.prepare(x_dev.view(torch.int16).cpu().numpy().view(np.uint16), dtype_code=1)
+    ref = O.mul_mat(qtype, w, k, act, m, threads=16)
+    out = gpu_mmq(kai, [(qtype, w, to_dev(w))], x_dev).cpu().numpy()
+    assert O.normwise_rel(out, ref) <= TOL_F32
+
+
 # ----------------------------------------------------------------- full BASELINE shapes
 
 FULL = [
