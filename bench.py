@@ -44,6 +44,9 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-prefill", action="store_true", help="skip the prefill leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--kernel-sample", action="store_true",
+                   help="counter-collection run: a 256 MiB device copy (calibration) and the dominant "
+                        "GEMV on each weight copy, eager launches only")
     return p.parse_args()
 
 
@@ -62,6 +65,9 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     batches = [int(b) for b in args.batches.split(",")]
+    if args.kernel_sample:
+        kernel_sample(lib, dev, batches)
+        return
 
     mats = [  # name, type, n, k
         ("gate_up", Q4_K, 34816, 5120),
@@ -223,6 +229,39 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
+
+
+def kernel_sample(lib, dev, batches):
+    """Eager launches for rocprofv3 --pmc runs: FETCH_SIZE / WRITE_SIZE of a plain copy of
+    known size (the calibration) next to those of the Q4_K gate/up GEMV per batch size."""
+    import torch
+
+    from kaillm_amd import native
+    from kaillm_amd.formats import Q4_K, quantize
+
+    n, k = 34816, 5120
+    g = torch.Generator(device=dev).manual_seed(1000)
+    w32 = torch.randn((n, k), generator=g, device=dev, dtype=torch.float32).mul_(0.02).cpu().numpy()
+    packed = torch.from_numpy(quantize(w32, Q4_K)).to(dev)
+    copies = [packed] + [packed.clone() for _ in range(COPIES - 1)]
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    x = torch.from_numpy(np.random.default_rng(2).standard_normal((max(batches), k)).astype(np.float16)).to(dev)
+    out = torch.empty((max(batches), n), dtype=torch.float32, device=dev)
+    act = torch.empty(lib.kai_fused_activation_bytes(max(batches), k, 0), dtype=torch.uint8, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    for m in batches:
+        if m > 8:
+            continue
+        native.check(lib, lib.kai_fused_prepare(x.data_ptr(), 2, m, k, k, act.data_ptr(), 0, s))
+        for c in copies:
+            native.check(lib, lib.kai_fused_mmvq(c.data_ptr(), Q4_K, n, k, m, act.data_ptr(), 0,
+                                                 out.data_ptr(), 0, n, s))
+    torch.cuda.synchronize()
+    print(f"[bench] kernel sample: 3 copies of {src.numel()} bytes, Q4_K {n}x{k} GEMV x{COPIES} "
+          f"at batch {[m for m in batches if m <= 8]}", flush=True)
 
 
 def cpu_baseline(w_dev, qtype, n, k, seconds):
