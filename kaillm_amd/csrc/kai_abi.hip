@@ -13,23 +13,8 @@ namespace {
 
 thread_local std::string last_error;
 
-struct Layout {
-    kai::block_q8_1 *y1;
-    kai::block_q8_1 *y2;
-    float *inverse;
-};
-
-Layout activation_layout(void *activation, int64_t m, int64_t k, int two_pass) {
-    char *base = static_cast<char *>(activation);
-    const size_t pass = kai::q8_1_pass_bytes(m, k);
-    return {reinterpret_cast<kai::block_q8_1 *>(base),
-            two_pass ? reinterpret_cast<kai::block_q8_1 *>(base + pass) : nullptr,
-            reinterpret_cast<float *>(base + pass * (two_pass ? 2 : 1))};
-}
-
-size_t activation_bytes(int64_t m, int64_t k, int two_pass) {
-    return kai::q8_1_pass_bytes(m, k) * (two_pass ? 2 : 1) + kai::align256(size_t(m) * sizeof(float));
-}
+using kai::activation_bytes;
+using kai::activation_layout;
 
 constexpr int MAX_FUSED_ROWS = 8;  // kai_fused_mmvq contract (reference MAX_COLS)
 constexpr int MAX_K_BLOCKS = 1024;  // k <= 32768, one preparation lane per 32 values
@@ -111,8 +96,8 @@ extern "C" int kai_fused_prepare(const void *x, int x_dtype, int64_t m, int64_t 
     return entry([&] {
         if (!x || !activation || m < 1 || m > INT_MAX || k <= 0 || k % kai::QK8_1 || k > INT_MAX || stride_x < k)
             throw kai::Error("Invalid fused activation preparation arguments");
-        const Layout l = activation_layout(activation, m, k, two_pass);
-        kai::launch_prepare(x, x_dtype, m, k, stride_x, l.y1, l.y2, l.inverse, stream_of(stream));
+        kai::launch_prepare(x, x_dtype, m, k, stride_x, activation_layout(activation, m, k, two_pass),
+                            stream_of(stream));
     });
 }
 
@@ -123,9 +108,12 @@ extern "C" int kai_fused_mmvq(const void *weight, int type, int64_t n, int64_t k
         if (!weight || !activation || !dst || !shape_ok(type, n, k, m, MAX_FUSED_ROWS) || stride_dst < n ||
             stride_dst > INT_MAX)
             throw kai::Error("Invalid fused MMVQ arguments");
-        const Layout l = activation_layout(const_cast<void *>(activation), m, k, two_pass);
-        kai::launch_mmvq(type, weight, n, k, m, l.y1, l.y2, l.inverse, dst, dst_bf16 != 0, stride_dst,
-                         stream_of(stream));
+        const kai::ActLayout l = activation_layout(const_cast<void *>(activation), m, k, two_pass);
+        if (!two_pass && m >= kai::MMQ_MIN_ROWS && k % 256 == 0)
+            kai::launch_mmq(type, weight, n, k, m, l.y1, l.inverse, dst, dst_bf16 != 0, stride_dst, stream_of(stream));
+        else
+            kai::launch_mmvq(type, weight, n, k, m, l.y1, l.y2, l.inverse, dst, dst_bf16 != 0, stride_dst,
+                             stream_of(stream));
     });
 }
 
@@ -160,8 +148,8 @@ extern "C" int kai_fused_mmq_run(const void *const *weights, const int *types, c
         if (hipGetDevice(&current) != hipSuccess) throw kai::Error("No HIP device");
         if (current != device && hipSetDevice(device) != hipSuccess) throw kai::Error("Invalid device index");
         const hipStream_t s = stream_of(stream);
-        const Layout l = activation_layout(scratch, m, k, 0);
-        kai::launch_prepare(x, x_dtype, m, k, stride_x, l.y1, nullptr, l.inverse, s);
+        const kai::ActLayout l = activation_layout(scratch, m, k, 0);
+        kai::launch_prepare(x, x_dtype, m, k, stride_x, l, s);
         const int64_t yrb = k / kai::QK8_1;
         const size_t elem = dst_bf16 ? 2 : 4;
         int64_t col = 0;

@@ -1,0 +1,235 @@
+// Weight side of the int8-MFMA kernels, per GGUF format: what one lane loads for one
+// 256-value K step of its weight row, the int8 codes of its octet of block kb (the MFMA
+// B operand), the fp32 scale of block kb, and the weight factors of the min terms.
+// Used by the batched MMQ kernel (kai_mmq.cuh). Arithmetic per format follows the
+// reference's block dots
+// vec_dot_*_q8_1 (in-tree text vllm_gguf_plugin/csrc/gguf/vecdotq.cuh, cited per format).
+#pragma once
+
+#include "kai_iq3s_grid.h"
+#include "kai_launch.h"
+#include "kai_units.h"
+
+namespace kai {
+
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+
+static __device__ const uint32_t mmq_iq3s_grid[512] = {KAI_IQ3S_GRID_VALUES};
+
+constexpr int MMQ_THREADS = 256;
+constexpr int MMQ_STEP = 256;  // values per K step (one superblock, or 8 blocks of 32)
+
+__device__ __forceinline__ uint64_t u64(uint2 v) { return uint64_t(v.x) | (uint64_t(v.y) << 32); }
+__device__ __forceinline__ uint32_t bits(uint32_t w, uint32_t shift, uint32_t width) {
+    return (w >> shift) & ((1u << width) - 1u);
+}
+
+
+// Weight side of the MMQ kernel, per format: what one lane loads for one K step of its
+// row (load), the int8 codes of its octet of block kb (codes), the scale of block kb
+// (scale: multiplies d8 * C), and the weight factors of the min terms (term: the B
+// operand of the fp32 MFMA for terms 4j .. 4j+3, the lane taking term 4j + oct).
+template <int TYPE> struct MmqW;
+
+// Q8_0: 8 blocks of 34 bytes per step. y += d8 * d * C. vecdotq.cuh:165-177.
+template <> struct MmqW<Q8_0> {
+    static constexpr int SB = 8 * 34, NTERM = 0;
+    static constexpr bool SPLIT16 = false;
+    struct Raw {
+        uint2 q[8];
+        uint32_t d[8];
+    };
+    static __device__ void load(Raw &r, const uint8_t *p, int o) {
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            r.d[b] = load_unaligned<uint16_t>(p + 34 * b);
+            r.q[b] = load_unaligned<uint2>(p + 34 * b + 2 + 8 * o);
+        }
+    }
+    static __device__ uint64_t codes(const Raw &r, int b, int, const uint32_t *) { return u64(r.q[b]); }
+    static __device__ float scale(const Raw &r, int b) { return half_bits_to_float(r.d[b]); }
+    static __device__ float term(const Raw &, int, int) { return 0.0f; }
+};
+
+// Q4_0: 8 blocks of 18 bytes; value v < 16 is the low nibble of qs[v], v >= 16 the high
+// nibble of qs[v - 16]. y += d * (d8 * C - 8 * s8), s8 the stored fp16 d8*sum(q8).
+// vecdotq.cuh:46-66.
+template <> struct MmqW<Q4_0> {
+    static constexpr int SB = 8 * 18, NTERM = 8;
+    static constexpr bool SPLIT16 = false;
+    struct Raw {
+        uint2 q[8];
+        uint32_t d[8];
+    };
+    static __device__ void load(Raw &r, const uint8_t *p, int o) {
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            r.d[b] = load_unaligned<uint16_t>(p + 18 * b);
+            r.q[b] = load_unaligned<uint2>(p + 18 * b + 2 + 8 * (o & 1));
+        }
+    }
+    static __device__ uint64_t codes(const Raw &r, int b, int o, const uint32_t *) {
+        return (u64(r.q[b]) >> (4 * (o >> 1))) & 0x0f0f0f0f0f0f0f0full;
+    }
+    static __device__ float scale(const Raw &r, int b) { return half_bits_to_float(r.d[b]); }
+    static __device__ float term(const Raw &r, int j, int o) {  // block 4j + o: -8 d
+        const uint32_t d = o == 0 ? r.d[4 * j] : o == 1 ? r.d[4 * j + 1] : o == 2 ? r.d[4 * j + 2] : r.d[4 * j + 3];
+        return -8.0f * half_bits_to_float(d);
+    }
+};
+
+// Q4_K superblock: d, dmin (fp16), 12 bytes of 6-bit scales/mins, qs[128]. Chunk c holds
+// blocks 2c (low nibbles) and 2c+1 (high nibbles); octet o of both is qs[32c + 8o, +8).
+// y += d8 * d * sc * C - dmin * m * (d8 * sum(q8)). vecdotq.cuh:328-351; scale packing
+// gguf-py quants.py:480-502.
+template <> struct MmqW<Q4_K> {
+    static constexpr int SB = 144, NTERM = 8;
+    static constexpr bool SPLIT16 = false;
+    struct Raw {
+        uint4 hdr;
+        uint2 q[4];
+    };
+    static __device__ void load(Raw &r, const uint8_t *p, int o) {
+        r.hdr = load_unaligned<uint4>(p);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) r.q[c] = load_unaligned<uint2>(p + 16 + 32 * c + 8 * o);
+    }
+    static __device__ uint64_t codes(const Raw &r, int b, int, const uint32_t *) {
+        const uint64_t q = u64(r.q[b / 2]);
+        return ((b & 1) ? q >> 4 : q) & 0x0f0f0f0f0f0f0f0full;
+    }
+    static __device__ float scale(const Raw &r, int b) {
+        const float d = half_bits_to_float(r.hdr.x & 0xffffu);
+        const uint32_t sc = b < 4 ? bits(r.hdr.y, 8 * b, 6)
+                                  : bits(r.hdr.w, 8 * (b - 4), 4) | (bits(r.hdr.y, 8 * (b - 4) + 6, 2) << 4);
+        return d * static_cast<float>(sc);
+    }
+    static __device__ float term(const Raw &r, int j, int o) {  // block 4j + o: -dmin * m
+        const float dmin = half_bits_to_float(r.hdr.x >> 16);
+        const uint32_t mn = j == 0 ? bits(r.hdr.z, 8 * o, 6)
+                                   : bits(r.hdr.w, 8 * o + 4, 4) | (bits(r.hdr.z, 8 * o + 6, 2) << 4);
+        return -dmin * static_cast<float>(mn);
+    }
+};
+
+// Q6_K superblock: ql[128], qh[64], int8 scales[16], d. Block kb = 4h + s, value v:
+// ql[64h + 32(s&1) + v] nibble s>>1, qh[32h + v] bits 2s; code q - 32 with one int8
+// scale per 16 values, so two MFMAs per block (the other half's codes zeroed) and the
+// two scales combined in 24-bit integer arithmetic. vecdotq.cuh:447-465; layout
+// gguf-py quants.py:553-573.
+template <> struct MmqW<Q6_K> {
+    static constexpr int SB = 210, NTERM = 0;
+    static constexpr bool SPLIT16 = true;
+    struct Raw {
+        uint2 ql[4];
+        uint2 qh[2];
+        uint4 sc;
+        uint32_t d;
+    };
+    static __device__ void load(Raw &r, const uint8_t *p, int o) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.ql[i] = load_unaligned<uint2>(p + 64 * (i / 2) + 32 * (i % 2) + 8 * o);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) r.qh[h] = load_unaligned<uint2>(p + 128 + 32 * h + 8 * o);
+        r.sc = load_unaligned<uint4>(p + 192);
+        r.d = load_unaligned<uint16_t>(p + 208);
+    }
+    static __device__ uint64_t codes(const Raw &r, int b, int, const uint32_t *) {
+        const int h = b / 4, s = b % 4;
+        const uint64_t ql = u64(r.ql[2 * h + (s & 1)]), qh = u64(r.qh[h]);
+        const uint64_t c = ((ql >> (4 * (s >> 1))) & 0x0f0f0f0f0f0f0f0full) | (((qh >> (2 * s)) & 0x0303030303030303ull) << 4);
+        // c - 32 per byte: flip bit 5 (6-bit two's complement), then sign-extend bit 5
+        const uint64_t t = c ^ 0x2020202020202020ull;
+        const uint64_t sign = t & 0x2020202020202020ull;
+        return t | (sign << 1) | (sign << 2);
+    }
+    static __device__ int iscale(const Raw &r, int g) {  // int8 scale of 16-value group g
+        const uint32_t w = g < 4 ? r.sc.x : g < 8 ? r.sc.y : g < 12 ? r.sc.z : r.sc.w;
+        return static_cast<int8_t>(bits(w, 8 * (g % 4), 8));
+    }
+    static __device__ float scale(const Raw &r, int) { return half_bits_to_float(r.d); }
+    static __device__ float term(const Raw &, int, int) { return 0.0f; }
+};
+
+// Q2_K superblock: scales[16] (low nibble scale, high nibble min, per 16 values),
+// qs[64], d, dmin. Block kb = 4h + s: code (qs[32h + v] >> 2s) & 3, multiplied by its
+// 4-bit scale (<= 45, no int8 overflow) so one MFMA covers both 16-value groups;
+// y += d8 * d * C' - dmin * (m_lo * d8 S_lo + m_hi * d8 S_hi). vecdotq.cuh:204-230;
+// layout gguf-py quants.py:407-429.
+template <> struct MmqW<Q2_K> {
+    static constexpr int SB = 84, NTERM = 16;
+    static constexpr bool SPLIT16 = false;
+    struct Raw {
+        uint4 sc;
+        uint2 q[2];
+        uint32_t dm;
+    };
+    static __device__ void load(Raw &r, const uint8_t *p, int o) {
+        r.sc = load_unaligned<uint4>(p);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) r.q[h] = load_unaligned<uint2>(p + 16 + 32 * h + 8 * o);
+        r.dm = load_unaligned<uint32_t>(p + 80);
+    }
+    static __device__ uint32_t word(const Raw &r, int i) { return i == 0 ? r.sc.x : i == 1 ? r.sc.y : i == 2 ? r.sc.z : r.sc.w; }
+    static __device__ uint64_t codes(const Raw &r, int b, int o, const uint32_t *) {
+        const int h = b / 4, s = b % 4;
+        const uint64_t q = (u64(r.q[h]) >> (2 * s)) & 0x0303030303030303ull;
+        // scale byte 2b + (o >> 1) lies in word b / 2
+        const uint32_t sc = bits(word(r, b / 2), 8 * (2 * (b & 1) + (o >> 1)), 4);
+        return q * sc;
+    }
+    static __device__ float scale(const Raw &r, int) { return half_bits_to_float(r.dm & 0xffffu); }
+    static __device__ float term(const Raw &r, int j, int o) {  // 16-value group 4j + o: -dmin * m
+        return -half_bits_to_float(r.dm >> 16) * static_cast<float>(bits(word(r, j), 8 * o + 4, 4));
+    }
+};
+
+// IQ3_S superblock: d, qs[64] (8-bit grid index low bits), qh[8], signs[32], scales[4].
+// Block kb, octet o: grid entries qs[8kb + 2o + i] | bit (2o + i) of qh[kb] << 8, signs
+// byte 4kb + o. y += d8 * d * (1 + 2 sc) * C. vecdotq.cuh:1649-1672; layout gguf-py
+// quants.py:1097-1125.
+template <> struct MmqW<IQ3_S> {
+    static constexpr int SB = 110, NTERM = 0;
+    static constexpr bool SPLIT16 = false;
+    struct Raw {
+        uint32_t qs[8];
+        uint32_t sg[8];
+        uint2 qh;
+        uint32_t sc;
+        uint32_t d;
+    };
+    static __device__ void load(Raw &r, const uint8_t *p, int o) {
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            r.qs[b] = load_unaligned<uint16_t>(p + 2 + 8 * b + 2 * o);
+            r.sg[b] = p[74 + 4 * b + o];
+        }
+        r.qh = load_unaligned<uint2>(p + 66);
+        r.sc = load_unaligned<uint32_t>(p + 106);
+        r.d = load_unaligned<uint16_t>(p);
+    }
+    static __device__ uint64_t codes(const Raw &r, int b, int o, const uint32_t *grid) {
+        const uint32_t qh = bits(b < 4 ? r.qh.x : r.qh.y, 8 * (b % 4), 8) >> (2 * o);
+        const uint32_t i0 = (r.qs[b] & 0xffu) | ((qh & 1u) << 8);
+        const uint32_t i1 = (r.qs[b] >> 8) | ((qh & 2u) << 7);
+        return uint64_t(Unit<IQ3_S>::signed_levels(grid[i0], r.sg[b] & 0x0fu)) |
+               (uint64_t(Unit<IQ3_S>::signed_levels(grid[i1], r.sg[b] >> 4)) << 32);
+    }
+    static __device__ float scale(const Raw &r, int b) {
+        return half_bits_to_float(r.d) * static_cast<float>(1 + 2 * static_cast<int>(bits(r.sc, 4 * b, 4)));
+    }
+    static __device__ float term(const Raw &, int, int) { return 0.0f; }
+};
+
+
+// The MMQ kernel's view of a format: MmqW plus the lane's activation octet and the
+// 16-value half it holds (used by the split Q6_K MFMA), and a post-load fix-up hook.
+template <int TYPE>
+struct MmqLoad : MmqW<TYPE> {
+    static __device__ int act_pos(int g) { return 8 * g; }
+    static __device__ bool first_half(int g) { return g < 2; }  // lanes holding values 0..15
+    static __device__ void fix(typename MmqW<TYPE>::Raw &) {}
+};
+
+}  // namespace kai

@@ -82,12 +82,19 @@ void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrow
     const uint8_t *wrow = weight + static_cast<int64_t>(min(row, nrows - 1)) * row_bytes;
     const int T = (units_per_row + G - 1) / G;
 
-    // Prime the ring first so the staging below overlaps the HBM latency.
+    // Prime the ring first so the staging below overlaps the HBM latency. Every load is
+    // unconditional (unit indices are clamped to the row; clamped units contribute zero),
+    // so the compiler's vmcnt waits are exact and DEPTH units per lane stay in flight.
+    const int last = units_per_row - 1;
+    auto load_unit = [&](typename U::W &w, int u) {
+        unit.load_w(w, wrow + static_cast<int64_t>(min(u, last) / U::PER_BLOCK) * BYTES);
+    };
     typename U::W ring[DEPTH];
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
-        const int u = gpos + G * d;
-        if (d < T && u < units_per_row) unit.load_w(ring[d], wrow + static_cast<int64_t>(u / U::PER_BLOCK) * BYTES);
+        load_unit(ring[d], gpos + G * d);
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     // Stage the IQ3_S grid, inverse[] and the activation: ROWS * nb blocks copied with
@@ -127,34 +134,35 @@ void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrow
 #pragma unroll
     for (int j = 0; j < M; ++j) acc[j] = 0.0f;
 
-    for (int t0 = 0; t0 < T; t0 += DEPTH) {
+    // T >= 1; a do-while keeps the prologue loads from being sunk behind a zero-trip check.
+    // The memory clobbers keep each unit's loads where they are issued and the scheduling
+    // barriers keep the next unit's arithmetic (and its load waits) out of this one.
+    const int TT = (T + DEPTH - 1) / DEPTH * DEPTH;
+    int t0 = 0;
+    do {
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
-            const int t = t0 + d;
-            if (t < T) {
-                const int u = gpos + G * t;
-                const bool live = u < units_per_row;
-                typename U::P w;
-                if (live) w = unit.prep(ring[d]);
-                const int un = u + G * DEPTH;
-                if (t + DEPTH < T && un < units_per_row)
-                    unit.load_w(ring[d], wrow + static_cast<int64_t>(un / U::PER_BLOCK) * BYTES);
-                if (live) {
-                    const int blk = u / U::PER_BLOCK;
+            const int u = gpos + G * (t0 + d);
+            const bool live = u < units_per_row;  // false for every unit past the row end
+            const typename U::P w = unit.prep(ring[d]);
+            load_unit(ring[d], u + G * DEPTH);
+            const int blk = min(u, last) / U::PER_BLOCK;
 #pragma unroll
-                    for (int j = 0; j < M; ++j) {
+            for (int j = 0; j < M; ++j) {
 #pragma unroll
-                        for (int p = 0; p < PASSES; ++p) {
-                            const int r = p * M + j;
-                            typename U::A a;
-                            unit.load_a(a, ActLds{act + size_t(r) * nb * 36, sums + size_t(r) * nb}, blk);
-                            acc[j] += unit.dot(w, a);
-                        }
-                    }
+                for (int p = 0; p < PASSES; ++p) {
+                    const int r = p * M + j;
+                    typename U::A a;
+                    unit.load_a(a, ActLds{act + size_t(r) * nb * 36, sums + size_t(r) * nb}, blk);
+                    const float v = unit.dot(w, a);
+                    acc[j] += live ? v : 0.0f;
                 }
             }
+            __asm__ volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
         }
-    }
+        t0 += DEPTH;
+    } while (t0 < TT);
 
     // Group totals; lane gpos of a group stores activation rows j = gpos, gpos + G, ...
 #pragma unroll
@@ -169,7 +177,7 @@ template <int TYPE, int M, bool TWO_PASS, int G>
 static void launch_variant(const uint8_t *w, int64_t n, int64_t k, const block_q8_1 *y1, const block_q8_1 *y2,
                            const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
     constexpr int THREADS = mmvq_threads<M>();
-    constexpr int DEPTH = 2;
+    constexpr int DEPTH = M <= 2 ? 3 : 2;
     constexpr int QK = block_elems(TYPE);
     const int64_t blocks_per_row = k / QK;
     const int64_t row_bytes = blocks_per_row * block_bytes(TYPE);

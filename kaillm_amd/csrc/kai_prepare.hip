@@ -135,27 +135,27 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prepare_q8_1_kernel(
 }
 
 template <int DTYPE>
-static void launch_prepare_dtype(const void *x, int64_t m, int64_t k, int64_t stride_x, block_q8_1 *y1,
-                                 block_q8_1 *y2, float *inverse, hipStream_t stream) {
+static void launch_prepare_dtype(const void *x, int64_t m, int64_t k, int64_t stride_x, const ActLayout &o,
+                                 hipStream_t stream) {
     const int nblocks = static_cast<int>(k / QK8_1);
     const int threads = (nblocks + WAVE - 1) / WAVE * WAVE;
     const auto *src = static_cast<const typename Src<DTYPE>::T *>(x);
-    if (y2) {
+    if (o.y2) {
         prepare_q8_1_kernel<DTYPE, true><<<dim3(static_cast<unsigned>(m)), dim3(threads), 0, stream>>>(
-            src, stride_x, static_cast<int>(k), y1, y2, inverse);
+            src, stride_x, static_cast<int>(k), o.y1, o.y2, o.inverse);
     } else {
         prepare_q8_1_kernel<DTYPE, false><<<dim3(static_cast<unsigned>(m)), dim3(threads), 0, stream>>>(
-            src, stride_x, static_cast<int>(k), y1, y2, inverse);
+            src, stride_x, static_cast<int>(k), o.y1, o.y2, o.inverse);
     }
 }
 
-void launch_prepare(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, block_q8_1 *y1,
-                    block_q8_1 *y2, float *inverse, hipStream_t stream) {
+void launch_prepare(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const ActLayout &out,
+                    hipStream_t stream) {
     if (k / QK8_1 > PREP_MAX_THREADS) throw Error("Fused activation preparation supports K <= 32768");
     switch (x_dtype) {
-        case 0: launch_prepare_dtype<0>(x, m, k, stride_x, y1, y2, inverse, stream); break;
-        case 1: launch_prepare_dtype<1>(x, m, k, stride_x, y1, y2, inverse, stream); break;
-        case 2: launch_prepare_dtype<2>(x, m, k, stride_x, y1, y2, inverse, stream); break;
+        case 0: launch_prepare_dtype<0>(x, m, k, stride_x, out, stream); break;
+        case 1: launch_prepare_dtype<1>(x, m, k, stride_x, out, stream); break;
+        case 2: launch_prepare_dtype<2>(x, m, k, stride_x, out, stream); break;
         default: throw Error("Fused activations must be F32, BF16 or F16");
     }
 }

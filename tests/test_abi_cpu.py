@@ -39,7 +39,7 @@ def test_supported(kai, args, want):
 
 
 def test_activation_bytes_matches_layout(kai):
-    for m, k, tp in ((1, 2048, 0), (3, 5120, 1), (16, 17408, 0), (2048, 5120, 0)):
+    for m, k, tp in ((1, 2048, 0), (3, 5120, 1), (16, 17408, 0), (2048, 5120, 0), (5, 96, 0)):
         assert kai.kai_fused_activation_bytes(m, k, tp) == O.activation_bytes(m, k, tp)
 
 
