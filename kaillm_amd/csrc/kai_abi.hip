@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <climits>
 #include <string>
+#include <vector>
 
 #include "../../include/kai_hip.h"
 #include "kai_launch.h"
@@ -57,6 +58,19 @@ Group validate_group(const int *types, const int64_t *rows, int count, int64_t k
     }
     if (g.total_rows % 4 || g.total_rows > INT_MAX) throw kai::Error("Fused MMQ output width must be a multiple of four");
     return g;
+}
+
+// Scratch of one fused MMQ call: the Q8_1 activation buffer, then, when a matrix of the
+// group may run on the fp16-MFMA GEMM, that GEMM's operands.
+size_t mmq_scratch_bytes(const int *types, const int64_t *rows, int count, int64_t k, int64_t m) {
+    bool mmf = false, t32 = false, t16 = false;
+    for (int i = 0; i < count; ++i) {
+        if (!kai::mmf_route(types[i], m, rows[i], k)) continue;
+        mmf = true;
+        t32 |= kai::mmf_uses_t32(types[i]);
+        t16 |= kai::mmf_uses_t16(types[i]);
+    }
+    return kai::activation_bytes(m, k, 0) + (mmf ? kai::mmf_bytes(m, k, t32, t16) : 0);
 }
 
 }  // namespace
@@ -124,7 +138,7 @@ extern "C" size_t kai_fused_mmq_workspace(int device, const int *types, const in
         last_error.clear();
         if (device < 0) throw kai::Error("Invalid device index");
         validate_group(types, rows, count, k, m);
-        return activation_bytes(m, k, 0);
+        return mmq_scratch_bytes(types, rows, count, k, m);
     } catch (const std::exception &error) {
         last_error = error.what();
         return 0;
@@ -137,7 +151,7 @@ extern "C" int kai_fused_mmq_run(const void *const *weights, const int *types, c
                                  uintptr_t stream) {
     return entry([&] {
         const Group g = validate_group(types, rows, count, k, m);
-        const size_t need = activation_bytes(m, k, 0);
+        const size_t need = mmq_scratch_bytes(types, rows, count, k, m);
         if (!weights || !x || !dst || !scratch || scratch_bytes < need || k % 4 || stride_x < k || device < 0)
             throw kai::Error("Invalid fused MMQ pointers, strides or scratch capacity");
         for (int i = 0; i < count; ++i)
@@ -149,13 +163,35 @@ extern "C" int kai_fused_mmq_run(const void *const *weights, const int *types, c
         if (current != device && hipSetDevice(device) != hipSuccess) throw kai::Error("Invalid device index");
         const hipStream_t s = stream_of(stream);
         const kai::ActLayout l = activation_layout(scratch, m, k, 0);
-        kai::launch_prepare(x, x_dtype, m, k, stride_x, l, s);
-        const int64_t yrb = k / kai::QK8_1;
         const size_t elem = dst_bf16 ? 2 : 4;
+        // Matrices on the fp16-MFMA GEMM (large m, supported format, 4-element aligned
+        // output columns) share one operand preparation; the others one Q8_1 preparation.
+        bool any_q8 = false, t32 = false, t16 = false;
+        std::vector<char> on_mmf(count);
+        {
+            int64_t c = 0;
+            for (int i = 0; i < count; ++i) {
+                const uintptr_t addr = reinterpret_cast<uintptr_t>(dst) + uintptr_t(c * elem);
+                on_mmf[i] = kai::mmf_route(types[i], m, rows[i], k) && ld % 4 == 0 && addr % (4 * elem) == 0;
+                any_q8 |= !on_mmf[i];
+                t32 |= on_mmf[i] && kai::mmf_uses_t32(types[i]);
+                t16 |= on_mmf[i] && kai::mmf_uses_t16(types[i]);
+                c += rows[i];
+            }
+        }
+        const kai::MmfAct fa =
+            kai::mmf_layout(static_cast<char *>(scratch) + activation_bytes(m, k, 0), m, k, t32, t16);
+        if (any_q8) kai::launch_prepare(x, x_dtype, m, k, stride_x, l, s);
+        bool prepared_mmf = false;
+        const int64_t yrb = k / kai::QK8_1;
         int64_t col = 0;
         for (int i = 0; i < count; ++i) {
             char *out = static_cast<char *>(dst) + col * elem;
-            if (k % 256 == 0) {
+            if (on_mmf[i]) {
+                if (!prepared_mmf) kai::launch_prepare_mmf(x, x_dtype, m, k, stride_x, fa, s);
+                prepared_mmf = true;
+                kai::launch_mmf(types[i], weights[i], rows[i], k, m, fa, out, dst_bf16 != 0, ld, s);
+            } else if (k % 256 == 0) {
                 kai::launch_mmq(types[i], weights[i], rows[i], k, m, l.y1, l.inverse, out, dst_bf16 != 0, ld, s);
             } else {
                 // k not a multiple of the 256-value MMQ step: GEMV launches of up to 16 rows

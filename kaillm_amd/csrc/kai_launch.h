@@ -59,4 +59,58 @@ constexpr int MMQ_MIN_ROWS = 3;
 void launch_mmq(int type, const void *weight, int64_t n, int64_t k, int64_t m, const block_q8_1 *y,
                 const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream);
 
+// Prefill GEMM on fp16 MFMA (kai_mmf.cuh) for K-quant weights from MMF_MIN_ROWS rows on.
+// Its activation operands, one region each, 256-aligned: a16 [m][k] fp16 = half(d8 * q8) of
+// the row's Q8_1 blocks; t32 [m][k/256][48 bytes] and t16 [m][k/256][96 bytes], the
+// min-term operands of 32- and 16-value sums (present when a matrix of the group needs
+// them); inverse [m] fp32.
+// Tiles of the fp16-MFMA GEMM (kai_mmf.cuh: 256 weight rows x 96 activation rows); below
+// MMF_MIN_TILES workgroups it fills too little of the chip and the int8 kernel is faster
+// (measured crossover on MI355X at 120-170 tiles).
+constexpr int MMF_TILE_N = 256, MMF_TILE_M = 96, MMF_MIN_TILES = 160;
+constexpr int MMF_MIN_ROWS = 128;
+struct MmfAct {
+    uint16_t *a16;
+    uint8_t *t32;
+    uint8_t *t16;
+    float *inverse;
+};
+bool mmf_supported(int type);
+inline bool mmf_uses_t32(int type) { return type == Q4_K; }
+inline bool mmf_uses_t16(int type) { return type == Q2_K; }
+// Whether an m-row product with this matrix runs on the fp16-MFMA GEMM (its weight is
+// addressed through one buffer descriptor: below 4 GiB).
+inline bool mmf_weight_fits(int type, int64_t n, int64_t k) {
+    return n * (k / 256) * block_bytes(type) <= int64_t(UINT32_MAX);
+}
+inline bool mmf_route(int type, int64_t m, int64_t n, int64_t k) {
+    const int64_t tiles = ((m + MMF_TILE_M - 1) / MMF_TILE_M) * ((n + MMF_TILE_N - 1) / MMF_TILE_N);
+    return mmf_supported(type) && m >= MMF_MIN_ROWS && tiles >= MMF_MIN_TILES && k % 256 == 0 &&
+           m * k * 2 <= INT32_MAX && n % 4 == 0 && mmf_weight_fits(type, n, k);
+}
+inline size_t mmf_bytes(int64_t m, int64_t k, bool t32, bool t16) {
+    return align256(size_t(m) * size_t(k) * 2) + (t32 ? align256(size_t(m) * size_t(k / 256) * 48) : 0) +
+           (t16 ? align256(size_t(m) * size_t(k / 256) * 96) : 0) + align256(size_t(m) * sizeof(float));
+}
+inline MmfAct mmf_layout(void *base, int64_t m, int64_t k, bool t32, bool t16) {
+    char *p = static_cast<char *>(base);
+    MmfAct a{};
+    a.a16 = reinterpret_cast<uint16_t *>(p);
+    p += align256(size_t(m) * size_t(k) * 2);
+    if (t32) {
+        a.t32 = reinterpret_cast<uint8_t *>(p);
+        p += align256(size_t(m) * size_t(k / 256) * 48);
+    }
+    if (t16) {
+        a.t16 = reinterpret_cast<uint8_t *>(p);
+        p += align256(size_t(m) * size_t(k / 256) * 96);
+    }
+    a.inverse = reinterpret_cast<float *>(p);
+    return a;
+}
+void launch_prepare_mmf(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const MmfAct &out,
+                        hipStream_t stream);
+void launch_mmf(int type, const void *weight, int64_t n, int64_t k, int64_t m, const MmfAct &act, void *dst,
+                bool dst_bf16, int64_t stride_dst, hipStream_t stream);
+
 }  // namespace kai

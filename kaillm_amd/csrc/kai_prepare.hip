@@ -51,19 +51,35 @@ __device__ __forceinline__ void load_block32(const typename Src<DTYPE>::T *p, fl
     }
 }
 
-// Quantise 32 normalised values into one Q8_1 block; returns the stored fp16 d.
-__device__ __forceinline__ float quantize_block(const float (&v)[32], block_q8_1 *out, int8_t (&q)[32]) {
+// Codes of one 32-value block: q = roundf(v / d) with d = max|v| / 127 (fp32), and the
+// stored fp16 d.
+struct BlockCodes {
+    float d;      // fp32 scale the codes were rounded with
+    uint16_t hd;  // its fp16 bits, the block's stored scale
+    int isum;     // sum of the codes
+};
+__device__ __forceinline__ BlockCodes block_codes(const float (&v)[32], int8_t (&q)[32]) {
     float a = 0.0f;
 #pragma unroll
     for (int j = 0; j < 32; ++j) a = fmaxf(a, fabsf(v[j]));
-    const float d = a / 127.0f;
-    int isum = 0;
+    BlockCodes b;
+    b.d = a / 127.0f;
+    b.isum = 0;
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
-        q[j] = static_cast<int8_t>(a == 0.0f ? 0.0f : roundf(v[j] / d));
-        isum += q[j];
+        q[j] = static_cast<int8_t>(a == 0.0f ? 0.0f : roundf(v[j] / b.d));
+        b.isum += q[j];
     }
-    const uint16_t hd = float_to_half_bits(d);
+    b.hd = float_to_half_bits(b.d);
+    return b;
+}
+
+// Quantise 32 normalised values into one Q8_1 block; returns the stored fp16 d.
+__device__ __forceinline__ float quantize_block(const float (&v)[32], block_q8_1 *out, int8_t (&q)[32]) {
+    const BlockCodes b = block_codes(v, q);
+    const float d = b.d;
+    const int isum = b.isum;
+    const uint16_t hd = b.hd;
     // half(d * sum) rounds the product to fp32 first, then to fp16. The backend would
     // otherwise fold fmul + fptrunc into one v_fma_mixlo_f16, which rounds once and
     // differs on exact fp16 ties; the empty asm makes the fp32 product opaque.
@@ -134,6 +150,70 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prepare_q8_1_kernel(
     }
 }
 
+// Min-term operands of sums over G values (G = 32 or 16) of one activation row: per
+// superblock, hi = half(t), lo = half(t - hi) and u as three runs of 256/G fp16 values,
+// where t = d8 * sum(q8) (exact in fp32) and u = sum(half(d8 q8) - d8 q8) over the G values.
+template <int G>
+__device__ __forceinline__ void store_min_operands(uint8_t *sb_base, int slot, float t, float u) {
+    constexpr int RUN = 2 * (256 / G);  // bytes per run
+    const uint16_t hi = float_to_half_bits(t);
+    const uint16_t lo = float_to_half_bits(t - half_bits_to_float(hi));
+    *reinterpret_cast<uint16_t *>(sb_base + 2 * slot) = hi;
+    *reinterpret_cast<uint16_t *>(sb_base + RUN + 2 * slot) = lo;
+    *reinterpret_cast<uint16_t *>(sb_base + 2 * RUN + 2 * slot) = float_to_half_bits(u);
+}
+
+// Operands of the fp16-MFMA prefill GEMM (kai_mmf.cuh), one workgroup per row: the row
+// scale and Q8_1 codes of prepare_q8_1_kernel (same arithmetic), written as
+// a16 = half(d8 * q8) with d8 the block's fp16 scale, plus the min-term operands of
+// 32-value sums (t32, 48 bytes per superblock) and of 16-value sums (t16, 96 bytes) when
+// those pointers are set. K is a multiple of 256.
+template <int DTYPE>
+__global__ __launch_bounds__(PREP_MAX_THREADS) void prepare_mmf_kernel(
+    const typename Src<DTYPE>::T *__restrict__ x, int64_t stride_x, int k, uint16_t *__restrict__ a16,
+    uint8_t *__restrict__ t32, uint8_t *__restrict__ t16, float *__restrict__ inverse) {
+    __shared__ float wave_max_lds[PREP_MAX_THREADS / WAVE];
+    const int row = blockIdx.x;
+    const int ib = threadIdx.x;
+    const int nblocks = k / QK8_1;
+    float v[32];
+    float bmax = 0.0f;
+    if (ib < nblocks) {
+        load_block32<DTYPE>(x + static_cast<int64_t>(row) * stride_x + static_cast<int64_t>(ib) * QK8_1, v);
+#pragma unroll
+        for (int j = 0; j < 32; ++j) bmax = fmaxf(bmax, fabsf(v[j]));
+    }
+    const float amax = block_max(bmax, wave_max_lds);
+    const float scale = row_scale_from_max(amax, inverse + row, threadIdx.x == 0);
+    if (ib >= nblocks) return;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) v[j] *= scale;
+    int8_t q[32];
+    const BlockCodes b = block_codes(v, q);
+    const float d8 = half_bits_to_float(b.hd);
+    uint32_t words[16];
+    float u[2] = {0.0f, 0.0f};
+    int s16[2] = {0, 0};
+#pragma unroll
+    for (int j = 0; j < 32; j += 2) {
+        const float e0 = d8 * static_cast<float>(q[j]), e1 = d8 * static_cast<float>(q[j + 1]);  // exact
+        const uint16_t h0 = float_to_half_bits(e0), h1 = float_to_half_bits(e1);
+        u[j / 16] += (half_bits_to_float(h0) - e0) + (half_bits_to_float(h1) - e1);
+        s16[j / 16] += q[j] + q[j + 1];
+        words[j / 2] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+    }
+    uint4 *dst = reinterpret_cast<uint4 *>(a16 + static_cast<int64_t>(row) * k + static_cast<int64_t>(ib) * QK8_1);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) dst[c] = make_uint4(words[4 * c], words[4 * c + 1], words[4 * c + 2], words[4 * c + 3]);
+    const int64_t sb = static_cast<int64_t>(row) * (k / 256) + ib / 8;
+    if (t32) store_min_operands<32>(t32 + sb * 48, ib % 8, d8 * static_cast<float>(b.isum), u[0] + u[1]);
+    if (t16) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            store_min_operands<16>(t16 + sb * 96, 2 * (ib % 8) + h, d8 * static_cast<float>(s16[h]), u[h]);
+    }
+}
+
 template <int DTYPE>
 static void launch_prepare_dtype(const void *x, int64_t m, int64_t k, int64_t stride_x, const ActLayout &o,
                                  hipStream_t stream) {
@@ -156,6 +236,33 @@ void launch_prepare(const void *x, int x_dtype, int64_t m, int64_t k, int64_t st
         case 0: launch_prepare_dtype<0>(x, m, k, stride_x, out, stream); break;
         case 1: launch_prepare_dtype<1>(x, m, k, stride_x, out, stream); break;
         case 2: launch_prepare_dtype<2>(x, m, k, stride_x, out, stream); break;
+        default: throw Error("Fused activations must be F32, BF16 or F16");
+    }
+}
+
+void launch_prepare_mmf(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const MmfAct &out,
+                        hipStream_t stream) {
+    if (k / QK8_1 > PREP_MAX_THREADS) throw Error("Fused activation preparation supports K <= 32768");
+    if (k % 256) throw Error("The fp16-MFMA GEMM needs K to be a multiple of 256");
+    const int nblocks = static_cast<int>(k / QK8_1);
+    const dim3 grid(static_cast<unsigned>(m)), block((nblocks + WAVE - 1) / WAVE * WAVE);
+    const int kk = static_cast<int>(k);
+    switch (x_dtype) {
+        case 0:
+            prepare_mmf_kernel<0><<<grid, block, 0, stream>>>(static_cast<const float *>(x), stride_x, kk, out.a16,
+                                                               out.t32, out.t16, out.inverse);
+            break;
+        case 1:
+        case 2: {
+            const auto *src = static_cast<const uint16_t *>(x);
+            if (x_dtype == 1)
+                prepare_mmf_kernel<1><<<grid, block, 0, stream>>>(src, stride_x, kk, out.a16, out.t32, out.t16,
+                                                                   out.inverse);
+            else
+                prepare_mmf_kernel<2><<<grid, block, 0, stream>>>(src, stride_x, kk, out.a16, out.t32, out.t16,
+                                                                   out.inverse);
+            break;
+        }
         default: throw Error("Fused activations must be F32, BF16 or F16");
     }
 }

@@ -252,6 +252,89 @@ def test_mmq_prefill_shape(kai, qtype):
     assert O.normwise_rel(out, ref) <= TOL_F32
 
 
+# Formats on the fp16-MFMA prefill GEMM. The library routes a matrix there from 160 tiles of
+# 96 activation rows x 256 weight rows on (fewer go to the int8 kernel), so these shapes
+# are large enough in m * n; k stays small for the CPU oracle.
+MMF_TYPES = [O.Q4_K]
+
+
+@pytest.mark.parametrize("qtype", MMF_TYPES, ids=lambda t: O.NAMES[t])
+@pytest.mark.parametrize("weights", ["random", "quantized"])
+@pytest.mark.parametrize("m,n,k", [(1000, 4100, 256), (960, 4096, 1280), (1100, 3840, 2048)])
+def test_mmf_parity(kai, qtype, weights, m, n, k):
+    """fp16-MFMA GEMM: exact and partial tiles in both dimensions (the last weight tile
+    one 4-row group, the last activation tile 40 rows), one to eight superblocks, wire
+    blocks from random bytes and from quantised N(0, 0.02) weights."""
+    print(f"mmf type={qtype} {weights} m={m} n={n} k={k}", flush=True)
+    rng = np.random.default_rng(qtype + m + n + k)
+    if weights == "random":
+        w = O.random_blocks(qtype, n, k, rng)
+    else:
+        from kaillm_amd.formats import quantize
+        w = quantize(rng.normal(0.0, 0.02, (n, k)).astype(np.float32), qtype)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    ref = O.mul_mat(qtype, w, k, O.prepare(x), m, threads=16)
+    out = gpu_mmq(kai, [(qtype, w, to_dev(w))], to_dev(x)).cpu().numpy()
+    err = O.normwise_rel(out, ref)
+    print(f"  normwise rel err {err:.3e}")
+    assert err <= TOL_F32
+
+
+def test_mmf_heavy_tailed_activations_bf16_out_and_stride(kai):
+    """Activations spread over many binades (small-scale blocks beside large ones) and
+    exact zeros; bf16 output into a wider matrix, the padding left untouched."""
+    rng = np.random.default_rng(5)
+    m, n, k = 960, 4096, 512
+    w = O.random_blocks(O.Q4_K, n, k, rng)
+    x = (rng.standard_normal((m, k)) * np.exp(rng.normal(0.0, 2.0, (m, k)))).astype(np.float32)
+    x[3] = 0.0
+    x[7, :512] = 0.0
+    act = O.prepare(x)
+    ref = O.mul_mat(O.Q4_K, w, k, act, m, threads=16)
+    out = gpu_mmq(kai, [(O.Q4_K, w, to_dev(w))], to_dev(x)).cpu().numpy()
+    assert np.all(out[3] == 0.0)
+    assert O.normwise_rel(out, ref) <= TOL_F32
+    outb = gpu_mmq(kai, [(O.Q4_K, w, to_dev(w))], to_dev(x), bf16=True, stride=n + 12).float().cpu().numpy()
+    assert O.normwise_rel(outb[:, :n], ref) <= TOL_BF16
+    assert np.isnan(outb[:, n:]).all()
+
+
+def test_mmf_group_with_int8_path(kai):
+    """A group where Q4_K matrices run on the fp16-MFMA GEMM (first and last) and the others
+    on the int8 kernel (one scratch, both preparations): Q6_K (format), a Q4_K after a column
+    offset of 2 mod 4 (unaligned output) and a narrow Q4_K (too few tiles, n = 2 mod 4)."""
+    rng = np.random.default_rng(11)
+    m, k = 1000, 512
+    mats = []
+    for qtype, n in ((O.Q4_K, 4096), (O.Q6_K, 130), (O.Q4_K, 4096), (O.Q4_K, 126), (O.Q4_K, 4096)):
+        w = O.random_blocks(qtype, n, k, rng)
+        mats.append((qtype, w, to_dev(w)))
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    ref = np.concatenate([O.mul_mat(t, w, k, O.prepare(x), m, threads=16) for t, w, _ in mats], axis=1)
+    out = gpu_mmq(kai, mats, to_dev(x)).cpu().numpy()
+    assert O.normwise_rel(out, ref) <= TOL_F32
+
+
+PREFILL = [("C4 Q4_K gate/up", O.Q4_K, 34816, 5120, 512), ("C4 Q4_K down", O.Q4_K, 5120, 17408, 1024)]
+
+
+@pytest.mark.parametrize("name,qtype,n,k,m", PREFILL, ids=[p[0] for p in PREFILL])
+def test_prefill_configs(kai, name, qtype, n, k, m):
+    """BASELINE config 4 weights (bf16 activations, quantised N(0, 0.02)) at m = 512 and, for
+    the narrow down projection, m = 1024 (both on the fp16-MFMA GEMM)."""
+    print(f"prefill {name} m={m}", flush=True)
+    from kaillm_amd.formats import quantize
+    rng = np.random.default_rng(n + m)
+    w = quantize(rng.normal(0.0, 0.02, (n, k)).astype(np.float32), qtype)
+    x_dev = to_dev(rng.standard_normal((m, k)).astype(np.float32)).to(torch.bfloat16)
+    act = O.prepare(x_dev.view(torch.int16).cpu().numpy().view(np.uint16), dtype_code=1)
+    ref = O.mul_mat(qtype, w, k, act, m, threads=16)
+    out = gpu_mmq(kai, [(qtype, w, to_dev(w))], x_dev).cpu().numpy()
+    err = O.normwise_rel(out, ref)
+    print(f"  normwise rel err {err:.3e}")
+    assert err <= TOL_F32
+
+
 # ----------------------------------------------------------------- full BASELINE shapes
 
 FULL = [
