@@ -61,14 +61,24 @@ void launch_mmq(int type, const void *weight, int64_t n, int64_t k, int64_t m, c
 
 // Prefill GEMM on fp16 MFMA (kai_mmf.cuh) for K-quant weights from MMF_MIN_ROWS rows on.
 // Its activation operands, one region each, 256-aligned: a16 [m][k] fp16 = half(d8 * q8) of
-// the row's Q8_1 blocks; t32 [m][k/256][48 bytes] and t16 [m][k/256][96 bytes], the
-// min-term operands of 32- and 16-value sums (present when a matrix of the group needs
-// them); inverse [m] fp32.
+// the row's Q8_1 blocks, in the GEMM's K order (mmf_a16_run); t32 [m][k/256][48 bytes] and
+// t16 [m][k/256][96 bytes], the min-term operands of 32- and 16-value sums (present when a
+// matrix of the group needs them); inverse [m] fp32.
 // Tiles of the fp16-MFMA GEMM (kai_mmf.cuh: 256 weight rows x 96 activation rows); below
 // MMF_MIN_TILES workgroups it fills too little of the chip and the int8 kernel is faster
 // (measured crossover on MI355X at 120-170 tiles).
 constexpr int MMF_TILE_N = 256, MMF_TILE_M = 96, MMF_MIN_TILES = 160;
 constexpr int MMF_MIN_ROWS = 128;
+// K order of a16 within a superblock, in runs of 8 values: the GEMM's step j (64 values)
+// holds at run 8 j + 4 h + g, for lane group g and half h, block 4 (j / 2) + 2 (g / 2) + h
+// at positions 16 (g % 2) + 8 (j % 2) + [0, 8). Every step then takes, per weight row and
+// lane group, 8 code bytes of one 16-byte run of the Q4_K superblock (a pair of steps
+// shares it), so a lane loads its codes as one 16-byte piece per two steps. Returns the
+// run of block `block` (0..7) positions [8 run, 8 run + 8).
+__host__ __device__ inline int mmf_a16_run(int block, int run) {
+    const int j = 2 * (block >> 2) + (run & 1), g = 2 * ((block >> 1) & 1) + (run >> 1), h = block & 1;
+    return 8 * j + 4 * h + g;
+}
 struct MmfAct {
     uint16_t *a16;
     uint8_t *t32;

@@ -105,11 +105,15 @@ __device__ __forceinline__ u4_t mmf_load16(__amdgpu_buffer_rsrc_t r, uint32_t vo
 // Wait until at most N vector-memory operations of this wave are outstanding; the tied
 // registers (loads issued before the N most recent operations) are valid afterwards.
 template <int N>
-__device__ __forceinline__ void mmf_wait(u2_t (&q)[4]) {
+__device__ __forceinline__ void mmf_wait() {
+    __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void mmf_wait(u4_t (&q)[4]) {
     __asm__ volatile("s_waitcnt vmcnt(%4)" : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]) : "n"(N) : "memory");
 }
 template <int N>
-__device__ __forceinline__ void mmf_wait(u2_t (&q)[4], u4_t &h) {
+__device__ __forceinline__ void mmf_wait(u4_t (&q)[4], u4_t &h) {
     __asm__ volatile("s_waitcnt vmcnt(%5)" : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]), "+v"(h) : "n"(N) : "memory");
 }
 // 16 bytes per lane from base + voff to LDS at lds + 16 * lane.
@@ -156,13 +160,11 @@ template <> struct MmfW<Q4_K> {
             r.scale2p = 0.0f;
             r.unit = need > 0.0f ? need : 1.0f;
         } else if (need > ad) {
-            int p = 0;
-            float u = ad;
-            while (u < need && p < 20) {
-                u *= 2.0f;
-                ++p;
-            }
-            r.unit = copysignf(u, d);
+            // Smallest p with ad 2^p >= need (1 <= p <= 20 here): ad 2^p0 has need's
+            // binary exponent, one more doubling when its mantissa is still below need's.
+            int p = __builtin_amdgcn_frexp_expf(need) - __builtin_amdgcn_frexp_expf(ad);
+            p += __builtin_amdgcn_ldexpf(ad, p) < need ? 1 : 0;
+            r.unit = copysignf(__builtin_amdgcn_ldexpf(ad, p), d);
             r.scale2p = __builtin_bit_cast(float, uint32_t(127 - p) << 23);
         }
         return r;
@@ -192,7 +194,8 @@ template <> struct MmfW<Q4_K> {
     }
     // Min-term row operands [e_hi(8) | e_lo(8) | f(8)], e = -dmin m / u, f = -8 sc 2^-P.
     static __device__ void min_row(u4_t h, const MmfRow &r, uint8_t *trow) {
-        const float dmin = half_bits_to_float(h.x >> 16);
+        // -dmin / u to within 2 ulp (one reciprocal): e keeps 22 of its bits in hi + lo.
+        const float ne = -half_bits_to_float(h.x >> 16) * __builtin_amdgcn_rcpf(r.unit);
         uint32_t eh[4], el[4], f[4];
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
@@ -200,7 +203,7 @@ template <> struct MmfW<Q4_K> {
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
                 const int b = 2 * p + s;
-                e[s] = -dmin * float(mn(h, b)) / r.unit;
+                e[s] = ne * float(mn(h, b));
                 fv[s] = -8.0f * float(sc(h, b)) * r.scale2p;
             }
             const uint32_t hb = pack_h2(e[0], e[1]);
@@ -263,8 +266,9 @@ __global__ __launch_bounds__(MMF_THREADS, 2) void mmf_kernel(
     const __amdgpu_buffer_rsrc_t hres =
         mmf_rsrc(weight + int64_t(n0) * row_bytes, uint32_t(min(MMF_NT, n - n0)) * uint32_t(row_bytes));
 
-    // Weight operand role: row col of each tile, bytes 8g of each step's 32 code bytes.
-    const uint32_t woff = uint32_t(col) * uint32_t(row_bytes) + 16u + 8u * g;
+    // Weight operand role: row col of each tile, code bytes [16g, 16g + 16) of each half
+    // superblock (steps 2p and 2p + 1 of its pair p).
+    const uint32_t woff = uint32_t(col) * uint32_t(row_bytes) + 16u + 16u * g;
     // Row-constant role: thread tid prepares row n0 + tid (rows past n read zeros: d = 0).
     const uint32_t hoff = uint32_t(tid) * uint32_t(row_bytes);
 
@@ -296,10 +300,10 @@ __global__ __launch_bounds__(MMF_THREADS, 2) void mmf_kernel(
             mmf_dma16(base, off, lds_addr(&tmins[(TINS * wave_u + i) * 1024]));
         }
     };
-    auto load_codes = [&](u2_t(&q)[4], int step) {
-        const uint32_t soff = uint32_t(step / 4) * F::SBB + 32u * uint32_t(step & 3);
+    auto load_codes = [&](u4_t(&q)[4], int pair) {  // pair p of superblock s: index 2 s + p
+        const uint32_t soff = uint32_t(pair >> 1) * F::SBB + 64u * uint32_t(pair & 1);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) q[t] = mmf_load8(tile_rsrc(t), woff, soff);
+        for (int t = 0; t < 4; ++t) q[t] = mmf_load16(tile_rsrc(t), woff, soff);
     };
     auto write_consts = [&](u4_t h, const MmfRow &r, int buf) {
 #pragma unroll
@@ -312,19 +316,21 @@ __global__ __launch_bounds__(MMF_THREADS, 2) void mmf_kernel(
 #pragma unroll
         for (int b = 0; b < MMF_MTILES; ++b) acc[a][b] = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Software pipeline, per wave and step j: [3 activation DMAs, 4 code loads] of step
-    // j + 2 (at a superblock's first step also [2 min-operand DMAs, 1 header load]); the
-    // end-of-step wait leaves exactly those in flight, so step j + 1's operands (and, at the
-    // second step, the header) have landed. Past the last step the loads repeat it.
-    constexpr int VM_STEP = AINS + 4, VM_SB = VM_STEP + TINS + 1;
-    u2_t codes[4][4];  // ring slot s & 3 holds step s's codes
+    // Software pipeline, per wave and step j: 3 activation DMAs of step j + 2; at a
+    // superblock's step 0 also the code loads of its steps 2-3, 2 min-operand DMAs and the
+    // next header, at its step 2 the code loads of the next superblock's steps 0-1. The
+    // end-of-step wait leaves only the current step's operations in flight, so step j + 1's
+    // operands have landed (and, at the end of step 1, the header issued at step 0). Past
+    // the last step the loads repeat it.
+    constexpr int VM_ACT = AINS, VM_CODES = AINS + 4, VM_SB = VM_CODES + TINS + 1;
+    u4_t codes[2][4];  // slot p holds pair p of the current superblock (16 bytes per tile)
     u4_t hdr = mmf_load16(hres, hoff, 0);
     issue_act(0, 0);
     load_codes(codes[0], 0);
     issue_act(min(1, steps - 1), 1);
-    load_codes(codes[1], min(1, steps - 1));
-    mmf_wait<VM_STEP>(codes[0], hdr);
-    write_consts(hdr, F::row(hdr), 0);
+    mmf_wait<VM_ACT>(codes[0], hdr);
+    MmfRow rnext = F::row(hdr);  // constants of the superblock the next step 0 starts
+    write_consts(hdr, rnext, 0);
     float unit_cur = 1.0f;
     __syncthreads();
 
@@ -334,29 +340,32 @@ __global__ __launch_bounds__(MMF_THREADS, 2) void mmf_kernel(
         for (int jj = 0; jj < 4; ++jj) {
             const int step = 4 * sb + jj, nx2 = min(step + 2, steps - 1);
             const int st2 = st == 0 ? 2 : st - 1;  // (step + 2) % 3
-            u2_t(&cur)[4] = codes[jj];
             // hdr holds superblock sb's header here: its min-term operands, read at the end.
             if (jj == 0) {
-                const MmfRow rcur = F::row(hdr);
-                F::min_row(hdr, rcur, &wmin[tid * TROW]);
-                unit_cur = rcur.unit;
+                F::min_row(hdr, rnext, &wmin[tid * TROW]);
+                unit_cur = rnext.unit;
             }
             issue_act(nx2, st2);
-            load_codes(codes[(jj + 2) & 3], nx2);
             if (jj == 0) {
+                load_codes(codes[1], 2 * sb + 1);
                 issue_tmin(sb);
                 hdr = mmf_load16(hres, hoff, uint32_t(min(sb + 1, nsb - 1)) * F::SBB);
+            } else if (jj == 2) {
+                load_codes(codes[0], min(2 * sb + 2, 2 * nsb - 1));
             }
 
             const uint8_t *as = a16s[st];
+            const int cpair = 2 * (jj >> 1) + (g >> 1);  // block pair of this lane group
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                // Weight operands of block 2 jj + b.
+                // Weight operands: block 2 cpair + b, positions 16 (g & 1) + 8 (jj & 1) + [0, 8).
                 h8_t wf[4];
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    const uint32_t kc = reinterpret_cast<const uint32_t *>(&wconst[sb & 1][64 * wave + 16 * t + col][jj])[b];
-                    wf[t] = b == 0 ? F::template frag<0>(cur[t], kc) : F::template frag<1>(cur[t], kc);
+                    const u4_t &pq = codes[jj >> 1][t];
+                    const u2_t cq = (jj & 1) ? u2_t{pq.z, pq.w} : u2_t{pq.x, pq.y};
+                    const uint32_t kc = reinterpret_cast<const uint32_t *>(&wconst[sb & 1][64 * wave + 16 * t + col][cpair])[b];
+                    wf[t] = b == 0 ? F::template frag<0>(cq, kc) : F::template frag<1>(cq, kc);
                 }
                 const int pc = 16 * ((4 * b + g) ^ swz_col);
 #pragma unroll
@@ -390,21 +399,22 @@ __global__ __launch_bounds__(MMF_THREADS, 2) void mmf_kernel(
 
             if (jj == 2) {  // the header of superblock sb + 1 landed at the end of step 1
                 if (sb + 1 < nsb) {
-                    const MmfRow rn = F::row(hdr);
-                    write_consts(hdr, rn, (sb + 1) & 1);
-                    ratio[tid] = unit_cur / rn.unit;
+                    rnext = F::row(hdr);
+                    write_consts(hdr, rnext, (sb + 1) & 1);
+                    ratio[tid] = unit_cur * __builtin_amdgcn_rcpf(rnext.unit);  // within 2 ulp
                 } else {
                     ratio[tid] = unit_cur;
                 }
             }
-            // Step j + 1's operands have landed (at the end of step 1 also the min operands
-            // and the header issued at step 0); only this step's operations stay in flight.
+            // Step j + 1's operands have landed; only this step's operations stay in flight.
             if (jj == 0)
-                mmf_wait<VM_SB>(codes[1]);
+                mmf_wait<VM_SB>();
             else if (jj == 1)
-                mmf_wait<VM_STEP>(codes[2], hdr);
+                mmf_wait<VM_ACT>(codes[1], hdr);
+            else if (jj == 2)
+                mmf_wait<VM_CODES>();
             else
-                mmf_wait<VM_STEP>(codes[(jj + 1) & 3]);
+                mmf_wait<VM_ACT>(codes[0]);
             __syncthreads();
             st = st == 2 ? 0 : st + 1;
         }

@@ -202,9 +202,11 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prepare_mmf_kernel(
         s16[j / 16] += q[j] + q[j + 1];
         words[j / 2] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
     }
-    uint4 *dst = reinterpret_cast<uint4 *>(a16 + static_cast<int64_t>(row) * k + static_cast<int64_t>(ib) * QK8_1);
+    // Runs of 8 values go to their place in the superblock's K order (mmf_a16_run).
+    uint4 *dst = reinterpret_cast<uint4 *>(a16 + static_cast<int64_t>(row) * k + static_cast<int64_t>(ib / 8) * 256);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) dst[c] = make_uint4(words[4 * c], words[4 * c + 1], words[4 * c + 2], words[4 * c + 3]);
+    for (int c = 0; c < 4; ++c)
+        dst[mmf_a16_run(ib % 8, c)] = make_uint4(words[4 * c], words[4 * c + 1], words[4 * c + 2], words[4 * c + 3]);
     const int64_t sb = static_cast<int64_t>(row) * (k / 256) + ib / 8;
     if (t32) store_min_operands<32>(t32 + sb * 48, ib % 8, d8 * static_cast<float>(b.isum), u[0] + u[1]);
     if (t16) {
