@@ -61,16 +61,26 @@ Group validate_group(const int *types, const int64_t *rows, int count, int64_t k
 }
 
 // Scratch of one fused MMQ call: the Q8_1 activation buffer, then, when a matrix of the
-// group may run on the fp16-MFMA GEMM, that GEMM's operands.
-size_t mmq_scratch_bytes(const int *types, const int64_t *rows, int count, int64_t k, int64_t m) {
+// group may run on an fp16-MFMA kernel, their operands, then the small-M GEMM's partial
+// sums (one buffer, reused by the matrices in turn).
+struct MmqScratch {
+    size_t act, mmf, partial;
+    size_t total() const { return act + mmf + partial; }
+};
+MmqScratch mmq_scratch(const int *types, const int64_t *rows, int count, int64_t k, int64_t m) {
     bool mmf = false, t32 = false, t16 = false;
+    size_t partial = 0;
     for (int i = 0; i < count; ++i) {
-        if (!kai::mmf_route(types[i], m, rows[i], k)) continue;
+        if (!kai::fp16_route(types[i], m, rows[i], k)) continue;
         mmf = true;
         t32 |= kai::mmf_uses_t32(types[i]);
         t16 |= kai::mmf_uses_t16(types[i]);
+        if (kai::mfv_route(types[i], m, rows[i], k)) partial = std::max(partial, kai::mfv_partial_bytes(m, rows[i], k));
     }
-    return kai::activation_bytes(m, k, 0) + (mmf ? kai::mmf_bytes(m, k, t32, t16) : 0);
+    return {kai::activation_bytes(m, k, 0), mmf ? kai::mmf_bytes(m, k, t32, t16) : 0, partial};
+}
+size_t mmq_scratch_bytes(const int *types, const int64_t *rows, int count, int64_t k, int64_t m) {
+    return mmq_scratch(types, rows, count, k, m).total();
 }
 
 }  // namespace
@@ -164,33 +174,39 @@ extern "C" int kai_fused_mmq_run(const void *const *weights, const int *types, c
         const hipStream_t s = stream_of(stream);
         const kai::ActLayout l = activation_layout(scratch, m, k, 0);
         const size_t elem = dst_bf16 ? 2 : 4;
-        // Matrices on the fp16-MFMA GEMM (large m, supported format, 4-element aligned
-        // output columns) share one operand preparation; the others one Q8_1 preparation.
+        // Matrices on the fp16-MFMA kernels (the prefill GEMM for large m with 4-element
+        // aligned output columns, the small-M GEMM up to 16 rows) share one operand
+        // preparation; the others one Q8_1 preparation.
+        enum : char { Q8 = 0, MMF = 1, MFV = 2 };
         bool any_q8 = false, t32 = false, t16 = false;
-        std::vector<char> on_mmf(count);
+        std::vector<char> path(count);
         {
             int64_t c = 0;
             for (int i = 0; i < count; ++i) {
                 const uintptr_t addr = reinterpret_cast<uintptr_t>(dst) + uintptr_t(c * elem);
-                on_mmf[i] = kai::mmf_route(types[i], m, rows[i], k) && ld % 4 == 0 && addr % (4 * elem) == 0;
-                any_q8 |= !on_mmf[i];
-                t32 |= on_mmf[i] && kai::mmf_uses_t32(types[i]);
-                t16 |= on_mmf[i] && kai::mmf_uses_t16(types[i]);
+                if (kai::mmf_route(types[i], m, rows[i], k) && ld % 4 == 0 && addr % (4 * elem) == 0) path[i] = MMF;
+                else if (kai::mfv_route(types[i], m, rows[i], k)) path[i] = MFV;
+                else path[i] = Q8;
+                any_q8 |= path[i] == Q8;
+                t32 |= path[i] != Q8 && kai::mmf_uses_t32(types[i]);
+                t16 |= path[i] != Q8 && kai::mmf_uses_t16(types[i]);
                 c += rows[i];
             }
         }
-        const kai::MmfAct fa =
-            kai::mmf_layout(static_cast<char *>(scratch) + activation_bytes(m, k, 0), m, k, t32, t16);
+        const MmqScratch plan = mmq_scratch(types, rows, count, k, m);
+        const kai::MmfAct fa = kai::mmf_layout(static_cast<char *>(scratch) + plan.act, m, k, t32, t16);
+        float *partial = reinterpret_cast<float *>(static_cast<char *>(scratch) + plan.act + plan.mmf);
         if (any_q8) kai::launch_prepare(x, x_dtype, m, k, stride_x, l, s);
         bool prepared_mmf = false;
         const int64_t yrb = k / kai::QK8_1;
         int64_t col = 0;
         for (int i = 0; i < count; ++i) {
             char *out = static_cast<char *>(dst) + col * elem;
-            if (on_mmf[i]) {
+            if (path[i] != Q8) {
                 if (!prepared_mmf) kai::launch_prepare_mmf(x, x_dtype, m, k, stride_x, fa, s);
                 prepared_mmf = true;
-                kai::launch_mmf(types[i], weights[i], rows[i], k, m, fa, out, dst_bf16 != 0, ld, s);
+                if (path[i] == MMF) kai::launch_mmf(types[i], weights[i], rows[i], k, m, fa, out, dst_bf16 != 0, ld, s);
+                else kai::launch_mfv(types[i], weights[i], rows[i], k, m, fa, partial, out, dst_bf16 != 0, ld, s);
             } else if (k % 256 == 0) {
                 kai::launch_mmq(types[i], weights[i], rows[i], k, m, l.y1, l.inverse, out, dst_bf16 != 0, ld, s);
             } else {

@@ -61,7 +61,7 @@ void launch_mmq(int type, const void *weight, int64_t n, int64_t k, int64_t m, c
 
 // Prefill GEMM on fp16 MFMA (kai_mmf.cuh) for K-quant weights from MMF_MIN_ROWS rows on.
 // Its activation operands, one region each, 256-aligned: a16 [m][k] fp16 = half(d8 * q8) of
-// the row's Q8_1 blocks, in the GEMM's K order (mmf_a16_run); t32 [m][k/256][48 bytes] and
+// the row's Q8_1 blocks, in the GEMM's K order (mmf_a16_run); t32 [m][k/256][64 bytes] and
 // t16 [m][k/256][96 bytes], the min-term operands of 32- and 16-value sums (present when a
 // matrix of the group needs them); inverse [m] fp32.
 // Tiles of the fp16-MFMA GEMM (kai_mmf.cuh: 256 weight rows x 96 activation rows); below
@@ -99,7 +99,7 @@ inline bool mmf_route(int type, int64_t m, int64_t n, int64_t k) {
            m * k * 2 <= INT32_MAX && n % 4 == 0 && mmf_weight_fits(type, n, k);
 }
 inline size_t mmf_bytes(int64_t m, int64_t k, bool t32, bool t16) {
-    return align256(size_t(m) * size_t(k) * 2) + (t32 ? align256(size_t(m) * size_t(k / 256) * 48) : 0) +
+    return align256(size_t(m) * size_t(k) * 2) + (t32 ? align256(size_t(m) * size_t(k / 256) * 64) : 0) +
            (t16 ? align256(size_t(m) * size_t(k / 256) * 96) : 0) + align256(size_t(m) * sizeof(float));
 }
 inline MmfAct mmf_layout(void *base, int64_t m, int64_t k, bool t32, bool t16) {
@@ -109,7 +109,7 @@ inline MmfAct mmf_layout(void *base, int64_t m, int64_t k, bool t32, bool t16) {
     p += align256(size_t(m) * size_t(k) * 2);
     if (t32) {
         a.t32 = reinterpret_cast<uint8_t *>(p);
-        p += align256(size_t(m) * size_t(k / 256) * 48);
+        p += align256(size_t(m) * size_t(k / 256) * 64);
     }
     if (t16) {
         a.t16 = reinterpret_cast<uint8_t *>(p);
@@ -120,6 +120,34 @@ inline MmfAct mmf_layout(void *base, int64_t m, int64_t k, bool t32, bool t16) {
 }
 void launch_prepare_mmf(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const MmfAct &out,
                         hipStream_t stream);
+
+// Small-M GEMM on fp16 MFMA (kai_mfv.cuh), up to MFV_MAX_ROWS activation rows, on the
+// operands of launch_prepare_mmf. Workgroups of 64 weight rows; K is split over
+// mfv_splits(n, k) workgroups (doubling while there are fewer than two workgroups per CU of
+// a 256-CU device and every split keeps at least 4 superblocks), whose fp32 partial sums
+// ([splits][m][n], mfv_partial_bytes) are added by a second kernel.
+constexpr int MFV_MAX_ROWS = 16;
+inline int mfv_splits(int64_t n, int64_t k) {
+    const int64_t wgs = (n + 63) / 64, nsb = k / 256;
+    int ks = 1;
+    while (ks < 8 && wgs * ks < 512 && nsb / (2 * ks) >= 4) ks *= 2;
+    return ks;
+}
+inline size_t mfv_partial_bytes(int64_t m, int64_t n, int64_t k) {
+    const int ks = mfv_splits(n, k);
+    return ks > 1 ? align256(size_t(ks) * size_t(m) * size_t(n) * sizeof(float)) : 0;
+}
+bool mfv_supported(int type);
+inline bool mfv_route(int type, int64_t m, int64_t n, int64_t k) {
+    return mfv_supported(type) && m >= 1 && m <= MFV_MAX_ROWS && k % 256 == 0 && n <= INT32_MAX &&
+           mmf_weight_fits(type, n, k);
+}
+// Whether an m-row product with this matrix runs on one of the fp16-MFMA kernels.
+inline bool fp16_route(int type, int64_t m, int64_t n, int64_t k) {
+    return mmf_route(type, m, n, k) || mfv_route(type, m, n, k);
+}
+void launch_mfv(int type, const void *weight, int64_t n, int64_t k, int64_t m, const MmfAct &act, float *partial,
+                void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream);
 void launch_mmf(int type, const void *weight, int64_t n, int64_t k, int64_t m, const MmfAct &act, void *dst,
                 bool dst_bf16, int64_t stride_dst, hipStream_t stream);
 

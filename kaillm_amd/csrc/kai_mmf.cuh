@@ -138,35 +138,40 @@ template <int TYPE> struct MmfW;
 // qs[32c, +32)) and 2c + 1 (high nibbles); lane group g takes qs[32c + 8g, +8).
 template <> struct MmfW<Q4_K> {
     static constexpr int SBB = 144;  // superblock bytes
-    static constexpr int TROW = 48;  // bytes per row of min-term operands
+    static constexpr int TROW = 64;  // bytes per row of min-term operands (4 block pairs)
+    // 6-bit scale and min of block b (0..7) from the 12 scale bytes (h.y, h.z, h.w). Both
+    // layouts are computed and one is selected by bit arithmetic, so a block index that
+    // differs between lanes costs no divergent branch.
+    static __device__ uint32_t pick(uint32_t lo4, uint32_t hi4, int b) {
+        const uint32_t m = 0u - uint32_t(b >> 2);  // all ones for blocks 4..7
+        return (lo4 & ~m) | (hi4 & m);
+    }
     static __device__ uint32_t sc(u4_t h, int b) {
-        return b < 4 ? bits(h.y, 8 * b, 6) : bits(h.w, 8 * (b - 4), 4) | (bits(h.y, 8 * (b - 4) + 6, 2) << 4);
+        const uint32_t j = 8u * uint32_t(b & 3);
+        return pick((h.y >> j) & 63u, ((h.w >> j) & 15u) | (((h.y >> (j + 6u)) & 3u) << 4), b);
     }
     static __device__ uint32_t mn(u4_t h, int b) {
-        return b < 4 ? bits(h.z, 8 * b, 6) : bits(h.w, 8 * (b - 4) + 4, 4) | (bits(h.z, 8 * (b - 4) + 6, 2) << 4);
+        const uint32_t j = 8u * uint32_t(b & 3);
+        return pick((h.z >> j) & 63u, ((h.w >> (j + 4u)) & 15u) | (((h.z >> (j + 6u)) & 3u) << 4), b);
     }
     // From the superblock header (d, dmin, scales): the unit u = d 2^P keeps
     // |e| = |dmin| m / |u| <= 64 * 63, with P = ceil(log2(|dmin| / (64 |d|))) when
     // positive. When that would exceed 20 (sc q 2^-P / 16 must stay a multiple of 2^-24,
     // exact in fp16), and for d = 0, the main term is dropped (it is then below 2^-21 of
     // the min term) and u = |dmin| / 64 (or 1).
-    static __device__ MmfRow row(u4_t h) {
+    static __device__ MmfRow row(u4_t h) {  // branch-free: selects, no divergence
         const float d = half_bits_to_float(h.x & 0xffffu), dmin = half_bits_to_float(h.x >> 16);
         const float ad = fabsf(d), need = fabsf(dmin) * 0.015625f;  // smallest |u| keeping e in range
+        // Smallest p with ad 2^p >= need when need > ad (1 <= p <= 20 where the main term
+        // is kept), else 0: ad 2^p0 has need's binary exponent, one more doubling when its
+        // mantissa is still below need's.
+        int p = __builtin_amdgcn_frexp_expf(need) - __builtin_amdgcn_frexp_expf(ad);
+        p += __builtin_amdgcn_ldexpf(ad, p) < need ? 1 : 0;
+        p = need > ad ? p : 0;
+        const bool drop = d == 0.0f || need > ad * 1048576.0f;
         MmfRow r;
-        r.unit = d;
-        r.scale2p = 1.0f;
-        if (d == 0.0f || need > ad * 1048576.0f) {
-            r.scale2p = 0.0f;
-            r.unit = need > 0.0f ? need : 1.0f;
-        } else if (need > ad) {
-            // Smallest p with ad 2^p >= need (1 <= p <= 20 here): ad 2^p0 has need's
-            // binary exponent, one more doubling when its mantissa is still below need's.
-            int p = __builtin_amdgcn_frexp_expf(need) - __builtin_amdgcn_frexp_expf(ad);
-            p += __builtin_amdgcn_ldexpf(ad, p) < need ? 1 : 0;
-            r.unit = copysignf(__builtin_amdgcn_ldexpf(ad, p), d);
-            r.scale2p = __builtin_bit_cast(float, uint32_t(127 - p) << 23);
-        }
+        r.unit = drop ? (need > 0.0f ? need : 1.0f) : copysignf(__builtin_amdgcn_ldexpf(ad, p), d);
+        r.scale2p = drop ? 0.0f : __builtin_bit_cast(float, uint32_t(127 - p) << 23);
         return r;
     }
     // Dequantisation constants of blocks b (even) and b + 1: fp16 pairs (mul, add) with
@@ -192,33 +197,29 @@ template <> struct MmfW<Q4_K> {
         }
         return __builtin_bit_cast(h8_t, u4_t{v[0], v[1], v[2], v[3]});
     }
-    // Min-term row operands [e_hi(8) | e_lo(8) | f(8)], e = -dmin m / u, f = -8 sc 2^-P.
-    static __device__ void min_row(u4_t h, const MmfRow &r, uint8_t *trow) {
+    // Min-term weight operand of block pair g (blocks 2g, 2g + 1): fp16
+    // [e_hi e_hi' e_hi e_hi' e_lo e_lo' f f'] with e = -dmin m / u = e_hi + e_lo and
+    // f = -8 sc 2^-P; the activation operand (prepare_mmf_kernel) is
+    // [t_hi t_hi' t_lo t_lo' t_hi t_hi' u8 u8'], so the MFMA's 8-value run of lane group g
+    // sums e t + f u8 over the pair (t = t_hi + t_lo; the e_lo t_lo term is below 2^-22).
+    static __device__ u4_t min_pair(u4_t h, const MmfRow &r, int g) {
         // -dmin / u to within 2 ulp (one reciprocal): e keeps 22 of its bits in hi + lo.
         const float ne = -half_bits_to_float(h.x >> 16) * __builtin_amdgcn_rcpf(r.unit);
-        uint32_t eh[4], el[4], f[4];
+        float e[2], fv[2];
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            float e[2], fv[2];
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const int b = 2 * p + s;
-                e[s] = ne * float(mn(h, b));
-                fv[s] = -8.0f * float(sc(h, b)) * r.scale2p;
-            }
-            const uint32_t hb = pack_h2(e[0], e[1]);
-            eh[p] = hb;
-            el[p] = pack_h2(e[0] - half_bits_to_float(hb & 0xffffu), e[1] - half_bits_to_float(hb >> 16));
-            f[p] = pack_h2(fv[0], fv[1]);
+        for (int s = 0; s < 2; ++s) {
+            e[s] = ne * float(mn(h, 2 * g + s));
+            fv[s] = -8.0f * float(sc(h, 2 * g + s)) * r.scale2p;
         }
-        *reinterpret_cast<u4_t *>(trow) = u4_t{eh[0], eh[1], eh[2], eh[3]};
-        *reinterpret_cast<u4_t *>(trow + 16) = u4_t{el[0], el[1], el[2], el[3]};
-        *reinterpret_cast<u4_t *>(trow + 32) = u4_t{f[0], f[1], f[2], f[3]};
+        const uint32_t hb = pack_h2(e[0], e[1]);
+        const uint32_t lb = pack_h2(e[0] - half_bits_to_float(hb & 0xffffu), e[1] - half_bits_to_float(hb >> 16));
+        return u4_t{hb, hb, lb, pack_h2(fv[0], fv[1])};
     }
-    // Operand chunk of lane group g in the min MFMA: weights [hi, hi, lo, f], activations
-    // [hi, lo, hi, u8].
-    static __device__ int wchunk(int g) { return g < 2 ? 0 : g - 1; }
-    static __device__ int tchunk(int g) { return g == 1 ? 1 : g == 3 ? 2 : 0; }
+    // All four pairs of one row (64 bytes), the layout the GEMM keeps in LDS.
+    static __device__ void min_row(u4_t h, const MmfRow &r, uint8_t *trow) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) *reinterpret_cast<u4_t *>(trow + 16 * g) = min_pair(h, r, g);
+    }
 };
 
 template <int TYPE>
@@ -381,10 +382,10 @@ __global__ __launch_bounds__(MMF_THREADS, 2) void mmf_kernel(
                 h8_t mw[4];
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
-                    mw[t] = *reinterpret_cast<const h8_t *>(&wmin[(64 * wave + 16 * t + col) * TROW + 16 * F::wchunk(g)]);
+                    mw[t] = *reinterpret_cast<const h8_t *>(&wmin[(64 * wave + 16 * t + col) * TROW + 16 * g]);
 #pragma unroll
                 for (int a = 0; a < MMF_MTILES; ++a) {
-                    const h8_t mt = *reinterpret_cast<const h8_t *>(&tmins[(16 * a + col) * TROW + 16 * F::tchunk(g)]);
+                    const h8_t mt = *reinterpret_cast<const h8_t *>(&tmins[(16 * a + col) * TROW + 16 * g]);
 #pragma unroll
                     for (int t = 0; t < 4; ++t)
                         acc[t][a] = __builtin_amdgcn_mfma_f32_16x16x32_f16(mw[t], mt, acc[t][a], 0, 0, 0);

@@ -150,23 +150,33 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prepare_q8_1_kernel(
     }
 }
 
-// Min-term operands of sums over G values (G = 32 or 16) of one activation row: per
-// superblock, hi = half(t), lo = half(t - hi) and u as three runs of 256/G fp16 values,
-// where t = d8 * sum(q8) (exact in fp32) and u = sum(half(d8 q8) - d8 q8) over the G values.
+// Min-term operands of one activation row, from t = d8 * sum(q8) (exact in fp32) and
+// u = sum(half(d8 q8) - d8 q8) over G values, hi = half(t), lo = half(t - hi):
+// G = 32 (t32): per superblock 4 block pairs of 8 fp16 [hi hi' lo lo' hi hi' u u'] (64
+// bytes), matching the weight operand [e_hi e_hi' e_hi e_hi' e_lo e_lo' f f'];
+// G = 16 (t16): per superblock three runs of 16 fp16 [hi | lo | u] (96 bytes).
 template <int G>
 __device__ __forceinline__ void store_min_operands(uint8_t *sb_base, int slot, float t, float u) {
-    constexpr int RUN = 2 * (256 / G);  // bytes per run
+    uint16_t *h = reinterpret_cast<uint16_t *>(sb_base);
     const uint16_t hi = float_to_half_bits(t);
     const uint16_t lo = float_to_half_bits(t - half_bits_to_float(hi));
-    *reinterpret_cast<uint16_t *>(sb_base + 2 * slot) = hi;
-    *reinterpret_cast<uint16_t *>(sb_base + RUN + 2 * slot) = lo;
-    *reinterpret_cast<uint16_t *>(sb_base + 2 * RUN + 2 * slot) = float_to_half_bits(u);
+    if constexpr (G == 32) {
+        uint16_t *pair = h + 8 * (slot / 2) + slot % 2;
+        pair[0] = hi;
+        pair[2] = lo;
+        pair[4] = hi;
+        pair[6] = float_to_half_bits(u);
+    } else {
+        h[slot] = hi;
+        h[16 + slot] = lo;
+        h[32 + slot] = float_to_half_bits(u);
+    }
 }
 
 // Operands of the fp16-MFMA prefill GEMM (kai_mmf.cuh), one workgroup per row: the row
 // scale and Q8_1 codes of prepare_q8_1_kernel (same arithmetic), written as
 // a16 = half(d8 * q8) with d8 the block's fp16 scale, plus the min-term operands of
-// 32-value sums (t32, 48 bytes per superblock) and of 16-value sums (t16, 96 bytes) when
+// 32-value sums (t32, 64 bytes per superblock) and of 16-value sums (t16, 96 bytes) when
 // those pointers are set. K is a multiple of 256.
 template <int DTYPE>
 __global__ __launch_bounds__(PREP_MAX_THREADS) void prepare_mmf_kernel(
@@ -208,7 +218,7 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prepare_mmf_kernel(
     for (int c = 0; c < 4; ++c)
         dst[mmf_a16_run(ib % 8, c)] = make_uint4(words[4 * c], words[4 * c + 1], words[4 * c + 2], words[4 * c + 3]);
     const int64_t sb = static_cast<int64_t>(row) * (k / 256) + ib / 8;
-    if (t32) store_min_operands<32>(t32 + sb * 48, ib % 8, d8 * static_cast<float>(b.isum), u[0] + u[1]);
+    if (t32) store_min_operands<32>(t32 + sb * 64, ib % 8, d8 * static_cast<float>(b.isum), u[0] + u[1]);
     if (t16) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)

@@ -335,6 +335,45 @@ def test_prefill_configs(kai, name, qtype, n, k, m):
     assert err <= TOL_F32
 
 
+# Small-M GEMM on fp16 MFMA (9..16 rows through the batched entry): K split across the
+# waves of a workgroup (small n), partial row tiles, one and an odd number of superblocks.
+@pytest.mark.parametrize("weights", ["random", "quantized"])
+@pytest.mark.parametrize("m,n,k", [(9, 1000, 256), (12, 200, 1280), (16, 4100, 2304), (13, 64, 5120)])
+def test_mfv_parity(kai, weights, m, n, k):
+    print(f"mfv m={m} n={n} k={k} {weights}", flush=True)
+    rng = np.random.default_rng(m * 7 + n + k)
+    if weights == "random":
+        w = O.random_blocks(O.Q4_K, n, k, rng)
+    else:
+        from kaillm_amd.formats import quantize
+        w = quantize(rng.normal(0.0, 0.02, (n, k)).astype(np.float32), O.Q4_K)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    ref = O.mul_mat(O.Q4_K, w, k, O.prepare(x), m, threads=16)
+    out = gpu_mmq(kai, [(O.Q4_K, w, to_dev(w))], to_dev(x)).cpu().numpy()
+    err = O.normwise_rel(out, ref)
+    print(f"  normwise rel err {err:.3e}")
+    assert err <= TOL_F32
+
+
+def test_mfv_heavy_tailed_bf16_out_stride_and_group(kai):
+    """Heavy-tailed activations, BF16 output into a wider merged tile, and a group that
+    mixes the small-M GEMM (Q4_K) with the int8 kernel (Q6_K) behind one preparation."""
+    m, k = 15, 1536
+    print(f"mfv group m={m} k={k}", flush=True)
+    rng = np.random.default_rng(77)
+    mats = []
+    for qtype, n in ((O.Q4_K, 520), (O.Q6_K, 72), (O.Q4_K, 36)):
+        w = O.random_blocks(qtype, n, k, rng)
+        mats.append((qtype, w, to_dev(w)))
+    x = (rng.standard_t(2.0, (m, k)) * 3.0).astype(np.float32)
+    ref = np.concatenate([O.mul_mat(t, w, k, O.prepare(x), m) for t, w, _ in mats], axis=1)
+    out = gpu_mmq(kai, mats, to_dev(x)).cpu().numpy()
+    assert O.normwise_rel(out, ref) <= TOL_F32
+    outb = gpu_mmq(kai, mats, to_dev(x), bf16=True, stride=ref.shape[1] + 4).float().cpu().numpy()
+    assert O.normwise_rel(outb[:, :ref.shape[1]], ref) <= TOL_BF16
+    assert np.isnan(outb[:, ref.shape[1]:]).all()
+
+
 # ----------------------------------------------------------------- full BASELINE shapes
 
 FULL = [
