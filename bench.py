@@ -98,6 +98,13 @@ def main():
         for c in range(COPIES):
             groups[(name, c)] = ((ctypes.c_void_p * 1)(weights[name][c].data_ptr()),
                                  (ctypes.c_int * 1)(qtype), (ctypes.c_int64 * 1)(n))
+    # scratch of the batched entry at the largest batch (its size query, as the reference's
+    # callers do)
+    mmq_ws = {}
+    for name, qtype, n, k in mats:
+        ptrs, types, rows = groups[(name, 0)]
+        size = lib.kai_fused_mmq_workspace(0, types, rows, 1, k, max_m, 1) if max_m > 8 else 0
+        mmq_ws[name] = torch.empty(max(size, 1), dtype=torch.uint8, device=dev)
 
     def projection(name, qtype, n, k, m, copy, s):
         x = xs[name][:m]
@@ -108,8 +115,8 @@ def main():
         else:
             ptrs, types, rows = groups[(name, copy)]
             native.check(lib, lib.kai_fused_mmq_run(ptrs, types, rows, 1, x.data_ptr(), 2, k, k, m,
-                                                    outs[name].data_ptr(), 0, 0, acts[name].data_ptr(),
-                                                    acts[name].numel(), 0, s))
+                                                    outs[name].data_ptr(), 0, 0, mmq_ws[name].data_ptr(),
+                                                    mmq_ws[name].numel(), 0, s))
 
     def capture(fn):
         g = torch.cuda.CUDAGraph()

@@ -3,8 +3,8 @@
 //
 // Reference: kai_dual::mmvq_dual (vllm_gguf_plugin/native/kernels/kai_dual_mmvq.cuh:258-327)
 // and its launcher (:329-397). Design for gfx950 instead of warp32 CTAs:
-//   * a wave64 works on 64/G rows at once, one group of G lanes per row (G = 8..64,
-//     chosen per shape so that short matrices with long rows still fill every CU);
+//   * a wave64 works on 64/G rows at once, one group of G lanes per row (G = 16..64,
+//     wider for long rows, pick_group);
 //     the lanes of a group walk the row's ~32-byte units (kai_units.h) in order, so
 //     each load instruction reads contiguous runs of G units of wire bytes;
 //   * a ring of DEPTH units per lane of wire bytes is kept in flight: unit t + DEPTH is
@@ -199,16 +199,16 @@ static void launch_variant(const uint8_t *w, int64_t n, int64_t k, const block_q
         dst_bf16 ? 1 : 0);
 }
 
-// Lanes per row: the smallest group that still yields about eight workgroups per CU
-// (short waves keep the tail of the launch short), widened only while a row keeps
-// more than 4 units per lane.
+// Lanes per row: 16, doubled while a row would leave more than 8 units per lane. A
+// group's loads then span 16-32 consecutive units (0.5-1 KiB) of its row, the shape
+// that streams best on MI355X (measured across G = 8..64 for every format and matrix
+// shape here); the grid size is secondary.
 template <int TYPE, int M>
 static int pick_group(int64_t n, int64_t k) {
+    (void)n;
     const int64_t units = (k / block_elems(TYPE)) * Unit<TYPE>::PER_BLOCK;
-    const int64_t target_blocks = int64_t(device_cu_count()) * 8;
-    const int waves = mmvq_threads<M>() / WAVE;
-    int g = 8;
-    while (g < 64 && (n + (waves * (WAVE / g)) - 1) / (waves * (WAVE / g)) < target_blocks && units / g > 4) g *= 2;
+    int g = 16;
+    while (g < 64 && units / g > 8) g *= 2;
     return g;
 }
 
@@ -216,7 +216,6 @@ template <int TYPE, int M, bool TWO_PASS>
 static void launch_group(const uint8_t *w, int64_t n, int64_t k, const block_q8_1 *y1, const block_q8_1 *y2,
                          const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
     switch (pick_group<TYPE, M>(n, k)) {
-        case 8: launch_variant<TYPE, M, TWO_PASS, 8>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream); break;
         case 16: launch_variant<TYPE, M, TWO_PASS, 16>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream); break;
         case 32: launch_variant<TYPE, M, TWO_PASS, 32>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream); break;
         default: launch_variant<TYPE, M, TWO_PASS, 64>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream); break;

@@ -11,94 +11,28 @@
 // Division is IEEE (hipcc's default correctly rounded fp32 divide), so the
 // bytes are identical to the CPU restatement.
 //
-// Launch: one workgroup per activation row, one lane per 32-value block, the row
-// read once into registers; wave64 reductions for the row maximum.
+// Launch: workgroups of 256 lanes, four lanes per 32-value block (8 values each), so
+// 64 blocks per workgroup and several workgroups per row; every workgroup of a row
+// reads the whole row for its maximum (L2-resident, a few KiB), which keeps the row
+// scale without a second launch, and the per-block maximum and code sum are quad
+// (DPP) reductions. The arithmetic per value is unchanged.
 #include "kai_launch.h"
 
 // Every rounding step must be the one the reference spells out. No floating-point
-// contraction in this file; see quantize_block for the fp16 conversion of d * sum.
+// contraction in this file; see quad_store for the fp16 conversion of d * sum.
 #pragma clang fp contract(off)
 
 namespace kai {
 
-constexpr int PREP_MAX_THREADS = 1024;  // K <= 32768
-
-template <int DTYPE>
-__device__ __forceinline__ void load_block32(const typename Src<DTYPE>::T *p, float (&v)[32]) {
-    if constexpr (DTYPE == 0) {
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const float4 f = load_unaligned<float4>(p + 4 * c);
-            v[4 * c + 0] = f.x; v[4 * c + 1] = f.y; v[4 * c + 2] = f.z; v[4 * c + 3] = f.w;
-        }
-    } else {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const uint4 u = load_unaligned<uint4>(p + 8 * c);
-            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t lo = w[i] & 0xffffu, hi = w[i] >> 16;
-                if constexpr (DTYPE == 1) {
-                    v[8 * c + 2 * i] = bf16_bits_to_float(lo);
-                    v[8 * c + 2 * i + 1] = bf16_bits_to_float(hi);
-                } else {
-                    v[8 * c + 2 * i] = half_bits_to_float(lo);
-                    v[8 * c + 2 * i + 1] = half_bits_to_float(hi);
-                }
-            }
-        }
-    }
-}
+constexpr int PREP_MAX_BLOCKS = 1024;  // K <= 32768 (the reference's limit)
 
 // Codes of one 32-value block: q = roundf(v / d) with d = max|v| / 127 (fp32), and the
-// stored fp16 d.
+// stored fp16 d (quad_codes).
 struct BlockCodes {
     float d;      // fp32 scale the codes were rounded with
     uint16_t hd;  // its fp16 bits, the block's stored scale
     int isum;     // sum of the codes
 };
-__device__ __forceinline__ BlockCodes block_codes(const float (&v)[32], int8_t (&q)[32]) {
-    float a = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) a = fmaxf(a, fabsf(v[j]));
-    BlockCodes b;
-    b.d = a / 127.0f;
-    b.isum = 0;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) {
-        q[j] = static_cast<int8_t>(a == 0.0f ? 0.0f : roundf(v[j] / b.d));
-        b.isum += q[j];
-    }
-    b.hd = float_to_half_bits(b.d);
-    return b;
-}
-
-// Quantise 32 normalised values into one Q8_1 block; returns the stored fp16 d.
-__device__ __forceinline__ float quantize_block(const float (&v)[32], block_q8_1 *out, int8_t (&q)[32]) {
-    const BlockCodes b = block_codes(v, q);
-    const float d = b.d;
-    const int isum = b.isum;
-    const uint16_t hd = b.hd;
-    // half(d * sum) rounds the product to fp32 first, then to fp16. The backend would
-    // otherwise fold fmul + fptrunc into one v_fma_mixlo_f16, which rounds once and
-    // differs on exact fp16 ties; the empty asm makes the fp32 product opaque.
-    float prod = d * static_cast<float>(isum);
-    __asm__ volatile("" : "+v"(prod));
-    const uint16_t hs = float_to_half_bits(prod);
-    uint32_t words[9];
-    words[0] = static_cast<uint32_t>(hd) | (static_cast<uint32_t>(hs) << 16);
-#pragma unroll
-    for (int w = 0; w < 8; ++w) {
-        words[1 + w] = static_cast<uint32_t>(static_cast<uint8_t>(q[4 * w])) |
-                       (static_cast<uint32_t>(static_cast<uint8_t>(q[4 * w + 1])) << 8) |
-                       (static_cast<uint32_t>(static_cast<uint8_t>(q[4 * w + 2])) << 16) |
-                       (static_cast<uint32_t>(static_cast<uint8_t>(q[4 * w + 3])) << 24);
-    }
-    __builtin_memcpy(out, words, sizeof(words));  // 36 bytes, 4-byte aligned
-    return half_bits_to_float(hd);
-}
-
 // Row scale from the row maximum: returns scale, writes inverse through lane 0.
 __device__ __forceinline__ float row_scale_from_max(float amax, float *inverse_out, bool writer) {
     const int biased = static_cast<int>((__builtin_bit_cast(uint32_t, amax) >> 23) & 255u);
@@ -120,33 +54,119 @@ __device__ __forceinline__ float block_max(float v, float *lds) {
     return m;
 }
 
+constexpr int PREP_THREADS = 256;
+constexpr int PREP_BLOCKS = PREP_THREADS / 4;  // 32-value blocks per workgroup
+
+// 8 consecutive source values as float.
+template <int DTYPE>
+__device__ __forceinline__ void load8(const typename Src<DTYPE>::T *p, float (&v)[8]) {
+    if constexpr (DTYPE == 0) {
+        const float4 a = load_unaligned<float4>(p), b = load_unaligned<float4>(p + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+        const uint4 u = load_unaligned<uint4>(p);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = DTYPE == 1 ? bf16_bits_to_float(w[i] & 0xffffu) : half_bits_to_float(w[i] & 0xffffu);
+            v[2 * i + 1] = DTYPE == 1 ? bf16_bits_to_float(w[i] >> 16) : half_bits_to_float(w[i] >> 16);
+        }
+    }
+}
+
+// Reductions over the four lanes of a block (every lane gets the same result).
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ float quad_max(float v) {
+    v = fmaxf(v, dpp_f32<DPP_QUAD_1032>(v));
+    return fmaxf(v, dpp_f32<DPP_QUAD_2301>(v));
+}
+__device__ __forceinline__ int quad_sum(int v) {
+    v += dpp_i32<DPP_QUAD_1032>(v);
+    return v + dpp_i32<DPP_QUAD_2301>(v);
+}
+__device__ __forceinline__ float quad_sum(float v) {
+    v += dpp_f32<DPP_QUAD_1032>(v);  // (v0 + v1) + (v2 + v3) in every lane
+    return v + dpp_f32<DPP_QUAD_2301>(v);
+}
+
+// Scale of a row from its maximum |x|, read by every workgroup of the row.
+template <int DTYPE>
+__device__ __forceinline__ float row_scale(const typename Src<DTYPE>::T *xr, int k, float *lds, float *inverse_out,
+                                           bool writer) {
+    float mx = 0.0f;
+    for (int p = threadIdx.x; p < k / 8; p += PREP_THREADS) {
+        float v[8];
+        load8<DTYPE>(xr + 8 * p, v);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[j]));
+    }
+    return row_scale_from_max(block_max(mx, lds), inverse_out, writer);
+}
+
+// Codes of the lane's 8 values of one block: d = max|v| / 127 over the block (quad),
+// q = roundf(v / d); returns the fp32 d, the stored fp16 bits and the block's code sum.
+__device__ __forceinline__ BlockCodes quad_codes(const float (&v)[8], int8_t (&q)[8]) {
+    float a = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(v[j]));
+    a = quad_max(a);
+    BlockCodes b;
+    b.d = a / 127.0f;
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        q[j] = static_cast<int8_t>(a == 0.0f ? 0.0f : roundf(v[j] / b.d));
+        s += q[j];
+    }
+    b.isum = quad_sum(s);
+    b.hd = float_to_half_bits(b.d);
+    return b;
+}
+
+// One Q8_1 block from the four lanes of a quad: part 0 writes (d, d * sum), each part
+// its 8 codes. Returns the stored fp16 d.
+__device__ __forceinline__ float quad_store(const float (&v)[8], block_q8_1 *out, int part, int8_t (&q)[8]) {
+    const BlockCodes b = quad_codes(v, q);
+    // half(d * sum) rounds the product to fp32 first, then to fp16 (no fused conversion).
+    float prod = b.d * static_cast<float>(b.isum);
+    __asm__ volatile("" : "+v"(prod));
+    const uint16_t hs = float_to_half_bits(prod);
+    uint32_t *w = reinterpret_cast<uint32_t *>(out);
+    if (part == 0) w[0] = static_cast<uint32_t>(b.hd) | (static_cast<uint32_t>(hs) << 16);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        w[1 + 2 * part + i] = static_cast<uint32_t>(static_cast<uint8_t>(q[4 * i])) |
+                              (static_cast<uint32_t>(static_cast<uint8_t>(q[4 * i + 1])) << 8) |
+                              (static_cast<uint32_t>(static_cast<uint8_t>(q[4 * i + 2])) << 16) |
+                              (static_cast<uint32_t>(static_cast<uint8_t>(q[4 * i + 3])) << 24);
+    return half_bits_to_float(b.hd);
+}
+
 template <int DTYPE, bool TWO_PASS>
-__global__ __launch_bounds__(PREP_MAX_THREADS) void prepare_q8_1_kernel(
+__global__ __launch_bounds__(PREP_THREADS) void prepare_q8_1_kernel(
     const typename Src<DTYPE>::T *__restrict__ x, int64_t stride_x, int k, block_q8_1 *__restrict__ y1,
     block_q8_1 *__restrict__ y2, float *__restrict__ inverse) {
-    __shared__ float wave_max_lds[PREP_MAX_THREADS / WAVE];
+    __shared__ float wave_max_lds[PREP_THREADS / WAVE];
     const int row = blockIdx.x;
-    const int ib = threadIdx.x;
     const int nblocks = k / QK8_1;
-    float v[32];
-    float bmax = 0.0f;
-    if (ib < nblocks) {
-        load_block32<DTYPE>(x + static_cast<int64_t>(row) * stride_x + static_cast<int64_t>(ib) * QK8_1, v);
+    const int part = threadIdx.x & 3, ib = blockIdx.y * PREP_BLOCKS + (threadIdx.x >> 2);
+    const auto *xr = x + static_cast<int64_t>(row) * stride_x;
+    const float scale = row_scale<DTYPE>(xr, k, wave_max_lds, inverse + row, blockIdx.y == 0 && threadIdx.x == 0);
+    if (ib >= nblocks) return;  // whole quads
+    float v[8];
+    load8<DTYPE>(xr + ib * QK8_1 + 8 * part, v);
 #pragma unroll
-        for (int j = 0; j < 32; ++j) bmax = fmaxf(bmax, fabsf(v[j]));
-    }
-    const float amax = block_max(bmax, wave_max_lds);
-    const float scale = row_scale_from_max(amax, inverse + row, threadIdx.x == 0);
-    if (ib >= nblocks) return;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) v[j] *= scale;
-    int8_t q1[32];
-    const float d1h = quantize_block(v, y1 + static_cast<int64_t>(row) * nblocks + ib, q1);
+    for (int j = 0; j < 8; ++j) v[j] *= scale;
+    int8_t q1[8];
+    const float d1h = quad_store(v, y1 + static_cast<int64_t>(row) * nblocks + ib, part, q1);
     if constexpr (TWO_PASS) {
 #pragma unroll
-        for (int j = 0; j < 32; ++j) v[j] = fmaf(-d1h, static_cast<float>(q1[j]), v[j]);
-        int8_t q2[32];
-        quantize_block(v, y2 + static_cast<int64_t>(row) * nblocks + ib, q2);
+        for (int j = 0; j < 8; ++j) v[j] = fmaf(-d1h, static_cast<float>(q1[j]), v[j]);
+        int8_t q2[8];
+        quad_store(v, y2 + static_cast<int64_t>(row) * nblocks + ib, part, q2);
     }
 }
 
@@ -173,56 +193,53 @@ __device__ __forceinline__ void store_min_operands(uint8_t *sb_base, int slot, f
     }
 }
 
-// Operands of the fp16-MFMA prefill GEMM (kai_mmf.cuh), one workgroup per row: the row
-// scale and Q8_1 codes of prepare_q8_1_kernel (same arithmetic), written as
+// Operands of the fp16-MFMA GEMMs (kai_mmf.cuh, kai_mfv.cuh): the row scale and Q8_1 codes
+// of prepare_q8_1_kernel (same arithmetic, same launch shape), written as
 // a16 = half(d8 * q8) with d8 the block's fp16 scale, plus the min-term operands of
 // 32-value sums (t32, 64 bytes per superblock) and of 16-value sums (t16, 96 bytes) when
 // those pointers are set. K is a multiple of 256.
 template <int DTYPE>
-__global__ __launch_bounds__(PREP_MAX_THREADS) void prepare_mmf_kernel(
+__global__ __launch_bounds__(PREP_THREADS) void prepare_mmf_kernel(
     const typename Src<DTYPE>::T *__restrict__ x, int64_t stride_x, int k, uint16_t *__restrict__ a16,
     uint8_t *__restrict__ t32, uint8_t *__restrict__ t16, float *__restrict__ inverse) {
-    __shared__ float wave_max_lds[PREP_MAX_THREADS / WAVE];
+    __shared__ float wave_max_lds[PREP_THREADS / WAVE];
     const int row = blockIdx.x;
-    const int ib = threadIdx.x;
     const int nblocks = k / QK8_1;
-    float v[32];
-    float bmax = 0.0f;
-    if (ib < nblocks) {
-        load_block32<DTYPE>(x + static_cast<int64_t>(row) * stride_x + static_cast<int64_t>(ib) * QK8_1, v);
+    const int part = threadIdx.x & 3, ib = blockIdx.y * PREP_BLOCKS + (threadIdx.x >> 2);
+    const auto *xr = x + static_cast<int64_t>(row) * stride_x;
+    const float scale = row_scale<DTYPE>(xr, k, wave_max_lds, inverse + row, blockIdx.y == 0 && threadIdx.x == 0);
+    if (ib >= nblocks) return;  // whole quads
+    float v[8];
+    load8<DTYPE>(xr + ib * QK8_1 + 8 * part, v);
 #pragma unroll
-        for (int j = 0; j < 32; ++j) bmax = fmaxf(bmax, fabsf(v[j]));
-    }
-    const float amax = block_max(bmax, wave_max_lds);
-    const float scale = row_scale_from_max(amax, inverse + row, threadIdx.x == 0);
-    if (ib >= nblocks) return;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) v[j] *= scale;
-    int8_t q[32];
-    const BlockCodes b = block_codes(v, q);
+    for (int j = 0; j < 8; ++j) v[j] *= scale;
+    int8_t q[8];
+    const BlockCodes b = quad_codes(v, q);
     const float d8 = half_bits_to_float(b.hd);
-    uint32_t words[16];
-    float u[2] = {0.0f, 0.0f};
-    int s16[2] = {0, 0};
+    uint32_t words[4];
+    float u = 0.0f;
+    int s = 0;
 #pragma unroll
-    for (int j = 0; j < 32; j += 2) {
+    for (int j = 0; j < 8; j += 2) {
         const float e0 = d8 * static_cast<float>(q[j]), e1 = d8 * static_cast<float>(q[j + 1]);  // exact
         const uint16_t h0 = float_to_half_bits(e0), h1 = float_to_half_bits(e1);
-        u[j / 16] += (half_bits_to_float(h0) - e0) + (half_bits_to_float(h1) - e1);
-        s16[j / 16] += q[j] + q[j + 1];
+        u += (half_bits_to_float(h0) - e0) + (half_bits_to_float(h1) - e1);
+        s += q[j] + q[j + 1];
         words[j / 2] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
     }
     // Runs of 8 values go to their place in the superblock's K order (mmf_a16_run).
     uint4 *dst = reinterpret_cast<uint4 *>(a16 + static_cast<int64_t>(row) * k + static_cast<int64_t>(ib / 8) * 256);
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-        dst[mmf_a16_run(ib % 8, c)] = make_uint4(words[4 * c], words[4 * c + 1], words[4 * c + 2], words[4 * c + 3]);
+    dst[mmf_a16_run(ib % 8, part)] = make_uint4(words[0], words[1], words[2], words[3]);
     const int64_t sb = static_cast<int64_t>(row) * (k / 256) + ib / 8;
-    if (t32) store_min_operands<32>(t32 + sb * 64, ib % 8, d8 * static_cast<float>(b.isum), u[0] + u[1]);
-    if (t16) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-            store_min_operands<16>(t16 + sb * 96, 2 * (ib % 8) + h, d8 * static_cast<float>(s16[h]), u[h]);
+    if (t32) {
+        const float ub = quad_sum(u);
+        if (part == 0) store_min_operands<32>(t32 + sb * 64, ib % 8, d8 * static_cast<float>(b.isum), ub);
+    }
+    if (t16) {  // 16-value halves: parts 0-1 and 2-3
+        const int s16 = s + dpp_i32<DPP_QUAD_1032>(s);
+        const float u16 = u + dpp_f32<DPP_QUAD_1032>(u);
+        if ((part & 1) == 0)
+            store_min_operands<16>(t16 + sb * 96, 2 * (ib % 8) + part / 2, d8 * static_cast<float>(s16), u16);
     }
 }
 
@@ -230,20 +247,20 @@ template <int DTYPE>
 static void launch_prepare_dtype(const void *x, int64_t m, int64_t k, int64_t stride_x, const ActLayout &o,
                                  hipStream_t stream) {
     const int nblocks = static_cast<int>(k / QK8_1);
-    const int threads = (nblocks + WAVE - 1) / WAVE * WAVE;
+    const dim3 grid(static_cast<unsigned>(m), static_cast<unsigned>((nblocks + PREP_BLOCKS - 1) / PREP_BLOCKS));
     const auto *src = static_cast<const typename Src<DTYPE>::T *>(x);
     if (o.y2) {
-        prepare_q8_1_kernel<DTYPE, true><<<dim3(static_cast<unsigned>(m)), dim3(threads), 0, stream>>>(
+        prepare_q8_1_kernel<DTYPE, true><<<grid, dim3(PREP_THREADS), 0, stream>>>(
             src, stride_x, static_cast<int>(k), o.y1, o.y2, o.inverse);
     } else {
-        prepare_q8_1_kernel<DTYPE, false><<<dim3(static_cast<unsigned>(m)), dim3(threads), 0, stream>>>(
+        prepare_q8_1_kernel<DTYPE, false><<<grid, dim3(PREP_THREADS), 0, stream>>>(
             src, stride_x, static_cast<int>(k), o.y1, o.y2, o.inverse);
     }
 }
 
 void launch_prepare(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const ActLayout &out,
                     hipStream_t stream) {
-    if (k / QK8_1 > PREP_MAX_THREADS) throw Error("Fused activation preparation supports K <= 32768");
+    if (k / QK8_1 > PREP_MAX_BLOCKS) throw Error("Fused activation preparation supports K <= 32768");
     switch (x_dtype) {
         case 0: launch_prepare_dtype<0>(x, m, k, stride_x, out, stream); break;
         case 1: launch_prepare_dtype<1>(x, m, k, stride_x, out, stream); break;
@@ -254,10 +271,11 @@ void launch_prepare(const void *x, int x_dtype, int64_t m, int64_t k, int64_t st
 
 void launch_prepare_mmf(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const MmfAct &out,
                         hipStream_t stream) {
-    if (k / QK8_1 > PREP_MAX_THREADS) throw Error("Fused activation preparation supports K <= 32768");
+    if (k / QK8_1 > PREP_MAX_BLOCKS) throw Error("Fused activation preparation supports K <= 32768");
     if (k % 256) throw Error("The fp16-MFMA GEMM needs K to be a multiple of 256");
     const int nblocks = static_cast<int>(k / QK8_1);
-    const dim3 grid(static_cast<unsigned>(m)), block((nblocks + WAVE - 1) / WAVE * WAVE);
+    const dim3 grid(static_cast<unsigned>(m), static_cast<unsigned>((nblocks + PREP_BLOCKS - 1) / PREP_BLOCKS)),
+        block(PREP_THREADS);
     const int kk = static_cast<int>(k);
     switch (x_dtype) {
         case 0:
