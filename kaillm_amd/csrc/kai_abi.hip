@@ -133,7 +133,7 @@ extern "C" int kai_fused_mmvq(const void *weight, int type, int64_t n, int64_t k
             stride_dst > INT_MAX)
             throw kai::Error("Invalid fused MMVQ arguments");
         const kai::ActLayout l = activation_layout(const_cast<void *>(activation), m, k, two_pass);
-        if (!two_pass && m >= kai::MMQ_MIN_ROWS && k % 256 == 0)
+        if (!two_pass && (m > kai::gemv_max_rows(type) || !kai::gemv_one_launch(m, k, 0)) && k % 256 == 0)
             kai::launch_mmq(type, weight, n, k, m, l.y1, l.inverse, dst, dst_bf16 != 0, stride_dst, stream_of(stream));
         else
             kai::launch_mmvq(type, weight, n, k, m, l.y1, l.y2, l.inverse, dst, dst_bf16 != 0, stride_dst,

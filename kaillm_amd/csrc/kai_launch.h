@@ -54,8 +54,20 @@ void launch_mmvq(int type, const void *weight, int64_t n, int64_t k, int64_t m, 
                  hipStream_t stream);
 
 // Batched GEMM (int8 MFMA), k % 256 == 0: dst[j*stride_dst + r] as above. kai_fused_mmvq uses
-// it from MMQ_MIN_ROWS rows on (below that the v_dot4 GEMV streams faster).
-constexpr int MMQ_MIN_ROWS = 3;
+// it above gemv_max_rows(type) rows; up to there the v_dot4 GEMV is faster (measured on
+// MI355X for every format at 3, 4 and 8 rows on the BASELINE shapes).
+inline int gemv_max_rows(int type) {
+    switch (type) {
+        case Q4_0: case Q8_0: case IQ3_S: return 8;
+        case Q4_K: case Q6_K: return 4;
+        default: return 3;
+    }
+}
+// Whether m activation rows fit the GEMV's LDS staging in one launch (more rows are split
+// into launches that each stream the weights again).
+inline bool gemv_one_launch(int64_t m, int64_t k, int two_pass) {
+    return m * (two_pass ? 2 : 1) * (k / QK8_1) * 40 <= 160 * 1024 - 4096;
+}
 void launch_mmq(int type, const void *weight, int64_t n, int64_t k, int64_t m, const block_q8_1 *y,
                 const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream);
 
