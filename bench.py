@@ -212,6 +212,15 @@ def main():
     if not args.no_cpu:
         cpu = cpu_baseline(weights[name][0], qtype, n, k, args.cpu_seconds)
 
+    # HBM bytes per launch of the same kernels, from the FETCH_SIZE / WRITE_SIZE counter runs
+    # (scaled by a plain copy's readings) summarised in profiles/.
+    traffic = None
+    tfile = ROOT / "profiles" / "gemv_q4k_34816x5120_traffic.json"
+    if tfile.exists():
+        tb = json.loads(tfile.read_text())["by_batch"]
+        if all(str(m) in tb for m in batches):
+            traffic = round(float(np.mean([tb[str(m)]["bytes"] for m in batches])))
+
     result = {
         "metric": "weight-stream HBM GB/s (% of peak) for Q4_K GEMV b1-16; prefill int8 TOPS",
         "value": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
@@ -229,7 +238,7 @@ def main():
                    "matrices": {nm: [n_, k_] for nm, _, n_, k_ in mats},
                    "step_weight_bytes": step_bytes, "weight_copies": COPIES},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "Q4_K gate/up GEMV 34816x5120 (mean over batch " + args.batches + ")",
                      "bytes_per_launch": wb, "avg_launch_us": round(avg_ms * 1e3, 2), "by_batch": by_m},
         "prefill": prefill,
@@ -259,16 +268,23 @@ def kernel_sample(lib, dev, batches):
     out = torch.empty((max(batches), n), dtype=torch.float32, device=dev)
     act = torch.empty(lib.kai_fused_activation_bytes(max(batches), k, 0), dtype=torch.uint8, device=dev)
     s = torch.cuda.current_stream().cuda_stream
+    types, rows = (ctypes.c_int * 1)(Q4_K), (ctypes.c_int64 * 1)(n)
     for m in batches:
-        if m > 8:
-            continue
-        native.check(lib, lib.kai_fused_prepare(x.data_ptr(), 2, m, k, k, act.data_ptr(), 0, s))
-        for c in copies:
-            native.check(lib, lib.kai_fused_mmvq(c.data_ptr(), Q4_K, n, k, m, act.data_ptr(), 0,
-                                                 out.data_ptr(), 0, n, s))
+        if m <= 8:
+            native.check(lib, lib.kai_fused_prepare(x.data_ptr(), 2, m, k, k, act.data_ptr(), 0, s))
+            for c in copies:
+                native.check(lib, lib.kai_fused_mmvq(c.data_ptr(), Q4_K, n, k, m, act.data_ptr(), 0,
+                                                     out.data_ptr(), 0, n, s))
+        else:
+            size = lib.kai_fused_mmq_workspace(0, types, rows, 1, k, m, 1)
+            scratch = torch.empty(size, dtype=torch.uint8, device=dev)
+            for c in copies:
+                ptrs = (ctypes.c_void_p * 1)(c.data_ptr())
+                native.check(lib, lib.kai_fused_mmq_run(ptrs, types, rows, 1, x.data_ptr(), 2, k, k, m,
+                                                        out.data_ptr(), 0, 0, scratch.data_ptr(), size, 0, s))
     torch.cuda.synchronize()
     print(f"[bench] kernel sample: 3 copies of {src.numel()} bytes, Q4_K {n}x{k} GEMV x{COPIES} "
-          f"at batch {[m for m in batches if m <= 8]}", flush=True)
+          f"at batch {batches}", flush=True)
 
 
 def cpu_baseline(w_dev, qtype, n, k, seconds):
