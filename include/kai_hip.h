@@ -47,6 +47,32 @@ size_t kai_fused_activation_bytes(int64_t m, int64_t k, int two_pass);
 int kai_fused_prepare(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x,
                       void *activation, int two_pass, uintptr_t stream);
 
+/* Single-pass activation of x[..., view] for m <= 8 rows: stored column c reads x column
+ * ((c/s)%a)*b*s + (c/(a*s))*s + c%s, i.e. x as [a][b][s] stored as [b][a][s]; s % 32 == 0,
+ * a*b*s == k. Same buffer layout and arithmetic as kai_fused_prepare with two_pass = 0.
+ * Replaces kai_fused_prepare_view (current_ggml_direct.cu:883-901; kernel
+ * kai_prepare_ext.cuh:121-140). */
+int kai_fused_prepare_view(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x,
+                           void *activation, int64_t a, int64_t b, int64_t s, uintptr_t stream);
+
+/* Single-pass activation of act[c] = rd(rd(silu(g[c])) * u[c]) for m <= 8 rows of a merged
+ * [m, 2k] gate_up input (row stride `stride` >= 2k; gate = columns [0, k), up = [k, 2k)), rd
+ * rounding to the input dtype, silu(g) = g / (1 + exp(-g)) with exp evaluated by a fixed
+ * sequence of IEEE operations (within 2 ulp). Replaces kai_fused_prepare_swiglu
+ * (current_ggml_direct.cu:903-919; kernel kai_prepare_ext.cuh:142-183). */
+int kai_fused_prepare_swiglu(const void *gate_up, int dtype, int64_t m, int64_t k, int64_t stride,
+                             void *activation, uintptr_t stream);
+
+/* Gemma RMSNorm for m <= 8 rows: v = x (+ residual; then v is written to residual_out, fp32
+ * [m, k]); y = bf16(v * rstd * weight32) with rstd = 1 / sqrt(sum(v^2) / k + eps) (IEEE divide
+ * and square root), written to y (bf16 [m, k]); the activation quantises the stored y. x and
+ * residual are F32 (0) or BF16 (1); y and residual_out are 16-byte aligned. Replaces
+ * kai_fused_norm_prepare (current_ggml_direct.cu:921-944; kernel kai_prepare_ext.cuh:185-251). */
+int kai_fused_norm_prepare(const void *x, int x_dtype, int64_t stride_x, const void *residual,
+                           int residual_dtype, int64_t stride_r, float *residual_out,
+                           const float *weight32, float eps, void *y, int64_t m, int64_t k,
+                           void *activation, uintptr_t stream);
+
 /* GEMV: dst[j * stride_dst + r] = inverse[j] * sum_b dot(W[r, b], q8[j, b]) for
  * r < n, j < m <= 8; F32 or BF16 (dst_bf16) output.
  * Replaces kai_fused_mmvq (current_ggml_direct.cu:946-965; kernel kai_dual_mmvq.cuh:258-397). */

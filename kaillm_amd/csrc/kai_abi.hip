@@ -125,6 +125,42 @@ extern "C" int kai_fused_prepare(const void *x, int x_dtype, int64_t m, int64_t 
     });
 }
 
+extern "C" int kai_fused_prepare_view(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x,
+                                      void *activation, int64_t a, int64_t b, int64_t s, uintptr_t stream) {
+    return entry([&] {
+        if (!x || !activation || m < 1 || m > MAX_FUSED_ROWS || k <= 0 || k % kai::QK8_1 || stride_x < k || s <= 0 ||
+            s % kai::QK8_1 || a <= 0 || b <= 0 || a * b * s != k)
+            throw kai::Error("Invalid fused view preparation arguments");
+        kai::launch_prepare_view(x, x_dtype, m, k, stride_x, a, b, s, activation_layout(activation, m, k, 0),
+                                 stream_of(stream));
+    });
+}
+
+extern "C" int kai_fused_prepare_swiglu(const void *gate_up, int dtype, int64_t m, int64_t k, int64_t stride,
+                                        void *activation, uintptr_t stream) {
+    return entry([&] {
+        if (!gate_up || !activation || m < 1 || m > MAX_FUSED_ROWS || k <= 0 || k % kai::QK8_1 || stride < 2 * k)
+            throw kai::Error("Invalid fused SwiGLU preparation arguments");
+        kai::launch_prepare_swiglu(gate_up, dtype, m, k, stride, activation_layout(activation, m, k, 0),
+                                   stream_of(stream));
+    });
+}
+
+extern "C" int kai_fused_norm_prepare(const void *x, int x_dtype, int64_t stride_x, const void *residual,
+                                      int residual_dtype, int64_t stride_r, float *residual_out,
+                                      const float *weight32, float eps, void *y, int64_t m, int64_t k,
+                                      void *activation, uintptr_t stream) {
+    return entry([&] {
+        if (!x || !y || !weight32 || !activation || m < 1 || m > MAX_FUSED_ROWS || k <= 0 || k % kai::QK8_1 ||
+            stride_x < k || (residual && (!residual_out || stride_r < k)))
+            throw kai::Error("Invalid fused norm preparation arguments");
+        if (reinterpret_cast<uintptr_t>(y) % 16 || reinterpret_cast<uintptr_t>(residual_out) % 16)
+            throw kai::Error("Fused norm outputs must be 16-byte aligned");
+        kai::launch_norm_prepare(x, x_dtype, stride_x, residual, residual_dtype, stride_r, residual_out, weight32, eps,
+                                 y, m, k, activation_layout(activation, m, k, 0), stream_of(stream));
+    });
+}
+
 extern "C" int kai_fused_mmvq(const void *weight, int type, int64_t n, int64_t k, int64_t m,
                               const void *activation, int two_pass, void *dst, int dst_bf16, int64_t stride_dst,
                               uintptr_t stream) {

@@ -47,6 +47,15 @@ inline ActLayout activation_layout(void *activation, int64_t m, int64_t k, int t
 
 void launch_prepare(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const ActLayout &out,
                     hipStream_t stream);
+// Fused producers of the single-pass activation (kai_prepare.hip): x[..., view], silu(gate)
+// * up from a merged [gate | up] row, and Gemma RMSNorm (+ residual) writing bf16 y.
+void launch_prepare_view(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, int64_t a, int64_t b,
+                         int64_t s, const ActLayout &out, hipStream_t stream);
+void launch_prepare_swiglu(const void *gate_up, int dtype, int64_t m, int64_t k, int64_t stride, const ActLayout &out,
+                           hipStream_t stream);
+void launch_norm_prepare(const void *x, int x_dtype, int64_t stride_x, const void *residual, int residual_dtype,
+                         int64_t stride_r, float *residual_out, const float *weight32, float eps, void *y, int64_t m,
+                         int64_t k, const ActLayout &out, hipStream_t stream);
 
 // GEMV: dst[j*stride_dst + r] = inverse[j] * sum_b dot(W[r, b], y[j, b]) for j < m <= 16.
 void launch_mmvq(int type, const void *weight, int64_t n, int64_t k, int64_t m, const block_q8_1 *y1,

@@ -297,4 +297,220 @@ void launch_prepare_mmf(const void *x, int x_dtype, int64_t m, int64_t k, int64_
     }
 }
 
+// ---------------------------------------------------------------- fused producers
+// Producers of the single-pass Q8_1 activation from a transformed input, so the consumer
+// GEMV needs no separate preparation (the reference's kai_prepare_ext.cuh:121-251, entry
+// points current_ggml_direct.cu:883-944):
+//   view   stored column c reads x column ((c/s)%a)*b*s + (c/(a*s))*s + c%s;
+//   swiglu act[c] = rd(rd(silu(g[c])) * u[c]) from a merged [gate | up] row, rd rounding to
+//          the input dtype, silu(g) = g / (1 + exp(-g));
+//   norm   v = x (+ r, written to the fp32 residual stream), y = bf16(v * rstd * w32) with
+//          rstd = 1 / sqrt(sum(v^2) / k + eps); the activation quantises the stored y.
+// One workgroup of PRODUCE_THREADS per row; run r of 8 values belongs to thread
+// r % PRODUCE_THREADS, so the four runs of a 32-value block sit in one quad. Every
+// reduction whose order could change a bit has a fixed order that the CPU oracle repeats:
+// sum(v^2) accumulates each thread's runs in order with fused multiply-adds, then a binary
+// tree over the 64 lanes of a wave, then the waves in order.
+constexpr int PRODUCE_THREADS = 512;
+constexpr int PRODUCE_RUNS = 8;  // k <= 32768
+
+// exp for the SwiGLU producer (the platform exp is not specified to the bit): Cody-Waite
+// reduction x = n ln2 + r with a two-part ln2, the degree-7 Taylor polynomial of e^r by
+// Horner in fused multiply-adds, and 2^n by ldexp. Each step is one IEEE operation, so the
+// oracle's copy of these lines returns the same bits; within 2 ulp of e^x.
+__device__ __forceinline__ float produce_expf(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return __builtin_inff();
+    if (x < -103.97208404541015625f) return 0.0f;
+    const float n = rintf(x * 1.44269502162933349609375f);
+    float r = fmaf(-n, 0.693145751953125f, x);
+    r = fmaf(-n, 1.42860682030941723212e-6f, r);
+    float p = 1.98412698e-4f;
+    p = fmaf(p, r, 1.38888889e-3f);
+    p = fmaf(p, r, 8.33333333e-3f);
+    p = fmaf(p, r, 4.16666667e-2f);
+    p = fmaf(p, r, 1.66666667e-1f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return ldexpf(p, static_cast<int>(n));
+}
+
+template <int DTYPE>
+__device__ __forceinline__ float round_to_src(float v) {
+    if constexpr (DTYPE == 1) return bf16_bits_to_float(float_to_bf16_bits(v));
+    else if constexpr (DTYPE == 2) return half_bits_to_float(float_to_half_bits(v));
+    else return v;
+}
+
+enum ProduceMode { PRODUCE_VIEW = 0, PRODUCE_SWIGLU = 1, PRODUCE_NORM = 2 };
+
+struct ProduceArgs {
+    const void *x;  // view: x; swiglu: [gate | up]; norm: x
+    int64_t stride_x;
+    const void *res;  // norm: residual or null
+    int64_t stride_r;
+    float *res_out;  // norm: fp32 residual stream [m][k]
+    const float *w32;
+    float eps;
+    uint16_t *y;  // norm: bf16 output [m][k]
+    int a, b, s;  // view
+    int k;
+    block_q8_1 *y1;
+    float *inverse;
+};
+
+// Sum over the workgroup in the fixed order described above (every lane gets it).
+__device__ __forceinline__ float produce_sum(float v, float *lds) {
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    v = wave_sum(v);  // binary tree over the lanes (pairs, quads, 8, 16, 32, 64)
+    if (lane == 0) lds[wave] = v;
+    __syncthreads();
+    float s = lds[0];
+    for (int w = 1; w < PRODUCE_THREADS / WAVE; ++w) s += lds[w];
+    return s;
+}
+
+template <int MODE, int XT, int RT>
+__global__ __launch_bounds__(PRODUCE_THREADS) void produce_kernel(ProduceArgs p) {
+    __shared__ float max_lds[PRODUCE_THREADS / WAVE];
+    __shared__ float sum_lds[PRODUCE_THREADS / WAVE];
+    using XS = typename Src<XT>::T;
+    const int row = blockIdx.x, t = threadIdx.x, k = p.k, nruns = k / 8;
+    const XS *xr = static_cast<const XS *>(p.x) + static_cast<int64_t>(row) * p.stride_x;
+    float v[PRODUCE_RUNS][8];
+    float amax = 0.0f, ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PRODUCE_RUNS; ++i) {
+        const int r = t + PRODUCE_THREADS * i, c = 8 * r;
+        if (r >= nruns) continue;
+        if constexpr (MODE == PRODUCE_VIEW) {
+            load8<XT>(xr + ((c / p.s) % p.a) * p.b * p.s + (c / (p.a * p.s)) * p.s + c % p.s, v[i]);
+        } else if constexpr (MODE == PRODUCE_SWIGLU) {
+            float u[8];
+            load8<XT>(xr + c, v[i]);
+            load8<XT>(xr + k + c, u);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float g = v[i][j];
+                v[i][j] = round_to_src<XT>(round_to_src<XT>(g / (1.0f + produce_expf(-g))) * u[j]);
+            }
+        } else {
+            load8<XT>(xr + c, v[i]);
+            if (p.res) {
+                float rv[8];
+                load8<RT>(static_cast<const typename Src<RT>::T *>(p.res) + static_cast<int64_t>(row) * p.stride_r + c, rv);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[i][j] += rv[j];
+                float4 *ro = reinterpret_cast<float4 *>(p.res_out + static_cast<int64_t>(row) * k + c);
+                ro[0] = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
+                ro[1] = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ss = fmaf(v[i][j], v[i][j], ss);
+        }
+        if constexpr (MODE != PRODUCE_NORM) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[i][j]));
+        }
+    }
+    if constexpr (MODE == PRODUCE_NORM) {
+        const float total = produce_sum(ss, sum_lds);
+        const float rstd = 1.0f / sqrtf(total / static_cast<float>(k) + p.eps);
+#pragma unroll
+        for (int i = 0; i < PRODUCE_RUNS; ++i) {
+            const int r = t + PRODUCE_THREADS * i, c = 8 * r;
+            if (r >= nruns) continue;
+            uint32_t packed[4];
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) {
+                const uint16_t h0 = float_to_bf16_bits(v[i][j] * rstd * p.w32[c + j]);
+                const uint16_t h1 = float_to_bf16_bits(v[i][j + 1] * rstd * p.w32[c + j + 1]);
+                v[i][j] = bf16_bits_to_float(h0);
+                v[i][j + 1] = bf16_bits_to_float(h1);
+                packed[j / 2] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+                amax = fmaxf(amax, fmaxf(fabsf(v[i][j]), fabsf(v[i][j + 1])));
+            }
+            *reinterpret_cast<uint4 *>(p.y + static_cast<int64_t>(row) * k + c) =
+                make_uint4(packed[0], packed[1], packed[2], packed[3]);
+        }
+    }
+    const float scale = row_scale_from_max(block_max(amax, max_lds), p.inverse + row, t == 0);
+#pragma unroll
+    for (int i = 0; i < PRODUCE_RUNS; ++i) {
+        const int r = t + PRODUCE_THREADS * i;
+        if (r >= nruns) continue;  // whole quads: nruns is a multiple of 4
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[i][j] *= scale;
+        int8_t q[8];
+        quad_store(v[i], p.y1 + static_cast<int64_t>(row) * (k / QK8_1) + r / 4, r & 3, q);
+    }
+}
+
+template <int MODE, int XT, int RT>
+static void launch_produce(const ProduceArgs &a, int64_t m, hipStream_t stream) {
+    produce_kernel<MODE, XT, RT><<<dim3(static_cast<unsigned>(m)), dim3(PRODUCE_THREADS), 0, stream>>>(a);
+}
+
+static ProduceArgs produce_args(int64_t k, const ActLayout &out) {
+    ProduceArgs a{};
+    a.k = static_cast<int>(k);
+    a.y1 = out.y1;
+    a.inverse = out.inverse;
+    return a;
+}
+
+void launch_prepare_view(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, int64_t a, int64_t b,
+                         int64_t s, const ActLayout &out, hipStream_t stream) {
+    if (k / 8 > PRODUCE_THREADS * PRODUCE_RUNS) throw Error("Fused activation preparation supports K <= 32768");
+    ProduceArgs p = produce_args(k, out);
+    p.x = x;
+    p.stride_x = stride_x;
+    p.a = static_cast<int>(a);
+    p.b = static_cast<int>(b);
+    p.s = static_cast<int>(s);
+    switch (x_dtype) {
+        case 0: launch_produce<PRODUCE_VIEW, 0, 0>(p, m, stream); break;
+        case 1: launch_produce<PRODUCE_VIEW, 1, 0>(p, m, stream); break;
+        case 2: launch_produce<PRODUCE_VIEW, 2, 0>(p, m, stream); break;
+        default: throw Error("Fused activations must be F32, BF16 or F16");
+    }
+}
+
+void launch_prepare_swiglu(const void *gate_up, int dtype, int64_t m, int64_t k, int64_t stride, const ActLayout &out,
+                           hipStream_t stream) {
+    if (k / 8 > PRODUCE_THREADS * PRODUCE_RUNS) throw Error("Fused activation preparation supports K <= 32768");
+    ProduceArgs p = produce_args(k, out);
+    p.x = gate_up;
+    p.stride_x = stride;
+    switch (dtype) {
+        case 0: launch_produce<PRODUCE_SWIGLU, 0, 0>(p, m, stream); break;
+        case 1: launch_produce<PRODUCE_SWIGLU, 1, 0>(p, m, stream); break;
+        case 2: launch_produce<PRODUCE_SWIGLU, 2, 0>(p, m, stream); break;
+        default: throw Error("Fused activations must be F32, BF16 or F16");
+    }
+}
+
+void launch_norm_prepare(const void *x, int x_dtype, int64_t stride_x, const void *residual, int residual_dtype,
+                         int64_t stride_r, float *residual_out, const float *weight32, float eps, void *y, int64_t m,
+                         int64_t k, const ActLayout &out, hipStream_t stream) {
+    if (k / 8 > PRODUCE_THREADS * PRODUCE_RUNS) throw Error("Fused activation preparation supports K <= 32768");
+    ProduceArgs p = produce_args(k, out);
+    p.x = x;
+    p.stride_x = stride_x;
+    p.res = residual;
+    p.stride_r = stride_r;
+    p.res_out = residual_out;
+    p.w32 = weight32;
+    p.eps = eps;
+    p.y = static_cast<uint16_t *>(y);
+    switch (x_dtype * 4 + (residual ? residual_dtype : 0)) {
+        case 0 * 4 + 0: launch_produce<PRODUCE_NORM, 0, 0>(p, m, stream); break;
+        case 0 * 4 + 1: launch_produce<PRODUCE_NORM, 0, 1>(p, m, stream); break;
+        case 1 * 4 + 0: launch_produce<PRODUCE_NORM, 1, 0>(p, m, stream); break;
+        case 1 * 4 + 1: launch_produce<PRODUCE_NORM, 1, 1>(p, m, stream); break;
+        default: throw Error("Fused norm inputs must be BF16 or F32 (residual BF16 or F32)");
+    }
+}
+
 }  // namespace kai

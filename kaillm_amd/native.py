@@ -33,6 +33,13 @@ def _load(path: str):
     lib.kai_fused_activation_bytes.restype = ctypes.c_size_t
     lib.kai_fused_prepare.argtypes = [ptr, c_int, i64, i64, i64, ptr, c_int, u64]
     lib.kai_fused_prepare.restype = c_int
+    lib.kai_fused_prepare_view.argtypes = [ptr, c_int, i64, i64, i64, ptr, i64, i64, i64, u64]
+    lib.kai_fused_prepare_view.restype = c_int
+    lib.kai_fused_prepare_swiglu.argtypes = [ptr, c_int, i64, i64, i64, ptr, u64]
+    lib.kai_fused_prepare_swiglu.restype = c_int
+    lib.kai_fused_norm_prepare.argtypes = [ptr, c_int, i64, ptr, c_int, i64, ptr, ptr, ctypes.c_float, ptr, i64,
+                                           i64, ptr, u64]
+    lib.kai_fused_norm_prepare.restype = c_int
     lib.kai_fused_mmvq.argtypes = [ptr, c_int, i64, i64, i64, ptr, c_int, ptr, c_int, i64, u64]
     lib.kai_fused_mmvq.restype = c_int
     lib.kai_fused_mmq_workspace.argtypes = [c_int, arr(c_int), arr(i64), c_int, i64, i64, c_int]

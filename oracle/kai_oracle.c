@@ -6,6 +6,7 @@
 #include "kai_oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "oracle_iq3s_grid.h"
@@ -182,6 +183,142 @@ int oracle_prepare(const void *x, int x_dtype, int64_t m, int64_t k, int64_t str
         }
     }
     return 0;
+}
+
+/* ---------------------------------------------------------------- fused producers */
+
+/* Round to nearest even; NaN -> quiet NaN with the sign and top payload bits kept. */
+uint16_t oracle_float_to_bf16(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+static float round_to_dtype(float v, int dtype) {
+    if (dtype == 1) return oracle_bf16_to_float(oracle_float_to_bf16(v));
+    if (dtype == 2) return oracle_half_to_float(oracle_float_to_half(v));
+    return v;
+}
+
+/*
+ * e^x as the SwiGLU producer evaluates it (the exp of the reference's silu,
+ * kai_prepare_ext.cuh:158, is CUDA's expf, whose bits are unspecified): Cody-Waite
+ * reduction x = n ln2 + r with ln2 split as 0.693145751953125 (exact in 16 bits) +
+ * 1.42860682030941723212e-6, e^r by its degree-7 Taylor polynomial in Horner form with
+ * fused multiply-adds, scaled by 2^n. Every line is one IEEE operation.
+ */
+float oracle_expf(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return INFINITY;
+    if (x < -103.97208404541015625f) return 0.0f;
+    const float n = rintf(x * 1.44269502162933349609375f);
+    float r = fmaf(-n, 0.693145751953125f, x);
+    r = fmaf(-n, 1.42860682030941723212e-6f, r);
+    float p = 1.98412698e-4f;
+    p = fmaf(p, r, 1.38888889e-3f);
+    p = fmaf(p, r, 8.33333333e-3f);
+    p = fmaf(p, r, 4.16666667e-2f);
+    p = fmaf(p, r, 1.66666667e-1f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return ldexpf(p, (int)n);
+}
+
+/*
+ * kai_dual::prepare_view (kai_prepare_ext.cuh:121-140, entry current_ggml_direct.cu:883-901):
+ * stored column c of row j is x[j, ((c/s)%a)*b*s + (c/(a*s))*s + c%s], then the single-pass
+ * Q8_1 preparation of those values (oracle_prepare with two_pass = 0).
+ */
+int oracle_prepare_view(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x,
+                        void *activation, int64_t a, int64_t b, int64_t s) {
+    if (!x || !activation || m < 1 || k <= 0 || k % QK8_1 || stride_x < k || s <= 0 || s % QK8_1 ||
+        a <= 0 || b <= 0 || a * b * s != k || x_dtype < 0 || x_dtype > 2)
+        return -1;
+    float *v = (float *)malloc((size_t)(m * k) * sizeof(float));
+    if (!v) return -1;
+    for (int64_t j = 0; j < m; ++j)
+        for (int64_t c = 0; c < k; ++c)
+            v[j * k + c] = load_x(x, x_dtype, j * stride_x + ((c / s) % a) * b * s + (c / (a * s)) * s + c % s);
+    const int rc = oracle_prepare(v, 0, m, k, k, activation, 0);
+    free(v);
+    return rc;
+}
+
+/*
+ * kai_dual::prepare_swiglu (kai_prepare_ext.cuh:142-183, entry current_ggml_direct.cu:903-919):
+ * act[c] = rd(rd(g / (1 + exp(-g))) * u) with g = row[c], u = row[k + c], rd rounding to
+ * the input dtype and exp = oracle_expf; then the single-pass Q8_1 preparation.
+ */
+int oracle_prepare_swiglu(const void *gate_up, int dtype, int64_t m, int64_t k, int64_t stride,
+                          void *activation) {
+    if (!gate_up || !activation || m < 1 || k <= 0 || k % QK8_1 || stride < 2 * k || dtype < 0 || dtype > 2)
+        return -1;
+    float *v = (float *)malloc((size_t)(m * k) * sizeof(float));
+    if (!v) return -1;
+    for (int64_t j = 0; j < m; ++j)
+        for (int64_t c = 0; c < k; ++c) {
+            const float g = load_x(gate_up, dtype, j * stride + c);
+            const float u = load_x(gate_up, dtype, j * stride + k + c);
+            v[j * k + c] = round_to_dtype(round_to_dtype(g / (1.0f + oracle_expf(-g)), dtype) * u, dtype);
+        }
+    const int rc = oracle_prepare(v, 0, m, k, k, activation, 0);
+    free(v);
+    return rc;
+}
+
+/*
+ * kai_dual::norm_prepare (kai_prepare_ext.cuh:185-251, entry current_ggml_direct.cu:921-944):
+ * v = x (+ r; v is stored to residual_out), y = bf16((v * rstd) * w32) with
+ * rstd = 1 / sqrt(sum(v^2) / k + eps), and the single-pass Q8_1 preparation of y.
+ * sum(v^2) is summed in the order the HIP producer uses (the reference's warp-shuffle order
+ * differs, so its y may differ from this one by one bf16 ulp where the product sits on a
+ * rounding boundary): 512 partial sums, partial t taking runs t, t + 512, ... of 8 values
+ * in order by fused multiply-adds; a pairwise tree over each 64 consecutive partials;
+ * the 8 tree sums added in order.
+ */
+int oracle_norm_prepare(const void *x, int x_dtype, int64_t stride_x, const void *residual,
+                        int residual_dtype, int64_t stride_r, float *residual_out,
+                        const float *weight32, float eps, uint16_t *y, int64_t m, int64_t k,
+                        void *activation) {
+    enum { THREADS = 512, LANES = 64 };
+    if (!x || !y || !weight32 || !activation || m < 1 || k <= 0 || k % QK8_1 || stride_x < k ||
+        (residual && (!residual_out || stride_r < k)) || x_dtype < 0 || x_dtype > 1 ||
+        (residual && (residual_dtype < 0 || residual_dtype > 1)) || k / 8 > (int64_t)THREADS * 8)
+        return -1;
+    float *v = (float *)malloc((size_t)(m * k) * sizeof(float));
+    if (!v) return -1;
+    for (int64_t j = 0; j < m; ++j) {
+        float *vr = v + j * k;
+        for (int64_t c = 0; c < k; ++c) {
+            vr[c] = load_x(x, x_dtype, j * stride_x + c);
+            if (residual) {
+                vr[c] += load_x(residual, residual_dtype, j * stride_r + c);
+                residual_out[j * k + c] = vr[c];
+            }
+        }
+        float part[THREADS];
+        for (int t = 0; t < THREADS; ++t) {
+            float ss = 0.0f;
+            for (int64_t r = t; r < k / 8; r += THREADS)
+                for (int e = 0; e < 8; ++e) ss = fmaf(vr[8 * r + e], vr[8 * r + e], ss);
+            part[t] = ss;
+        }
+        for (int width = 1; width < LANES; width *= 2)
+            for (int t = 0; t < THREADS; t += 2 * width) part[t] = part[t] + part[t + width];
+        float total = part[0];
+        for (int w = 1; w < THREADS / LANES; ++w) total += part[w * LANES];
+        const float rstd = 1.0f / sqrtf(total / (float)k + eps);
+        for (int64_t c = 0; c < k; ++c) {
+            const uint16_t h = oracle_float_to_bf16(vr[c] * rstd * weight32[c]);
+            y[j * k + c] = h;
+            vr[c] = oracle_bf16_to_float(h);
+        }
+    }
+    const int rc = oracle_prepare(v, 0, m, k, k, activation, 0);
+    free(v);
+    return rc;
 }
 
 /* ---------------------------------------------------------------- weight decoding */

@@ -17,14 +17,20 @@
  *   - the GEMV epilogue y[j, r] = inverse[j] * sum_b dot(W[r, b], q8[j, b])
  *     (kai_dual_mmvq.cuh:258-327);
  *   - block dequantization per gguf-py quants.py (:242-252, :397-402, :407-429,
- *     :476-523, :553-573, :1097-1125).
+ *     :476-523, :553-573, :1097-1125);
+ *   - the fused activation producers kai_dual::prepare_view / prepare_swiglu /
+ *     norm_prepare (kai_prepare_ext.cuh:121-251), with their two unspecified steps (exp,
+ *     and the order of the norm's sum of squares) fixed as the HIP kernels fix them.
  * Each function names the reference lines it follows.
  *
  * Pinning (tests/test_oracle_*.py): fp16/bf16 conversion against numpy; Q8_1
  * preparation against closed-form special cases and invariants; dequantization
  * against hand-assembled known-answer blocks; the block dots against
  * dequantize-then-dot in FP64 (an independent route through the layout); the
- * IQ3_S grid against the older vendored table (tests/golden/gen_iq3s_grid.py).
+ * IQ3_S grid against the older vendored table (tests/golden/gen_iq3s_grid.py); the
+ * producers against FP64 references (exp within 2 ulp of libm's double exp, RMSNorm
+ * within bf16 rounding), the view as a transposed copy prepared by oracle_prepare, and
+ * the SwiGLU dtype roundings against numpy's own conversions.
  */
 #ifndef KAI_ORACLE_H
 #define KAI_ORACLE_H
@@ -61,6 +67,26 @@ size_t oracle_activation_bytes(int64_t m, int64_t k, int two_pass);
 /* Q8_1 activation preparation. x_dtype: 0 f32, 1 bf16, 2 f16. Returns 0 or -1. */
 int oracle_prepare(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x,
                    void *activation, int two_pass);
+
+/* float -> bf16 bits (round to nearest even, NaN kept quiet). */
+uint16_t oracle_float_to_bf16(float f);
+
+/* e^x by the fixed operation sequence of the HIP SwiGLU producer (Cody-Waite + degree-7
+ * Taylor); within 2 ulp of e^x. */
+float oracle_expf(float x);
+
+/* Fused producers of the single-pass activation (returns 0 or -1):
+ * view (stored column c reads x column ((c/s)%a)*b*s + (c/(a*s))*s + c%s), SwiGLU of a
+ * merged [gate | up] row, and Gemma RMSNorm (+ residual) writing bf16 y and the fp32
+ * residual stream. The norm's sum of squares follows the HIP kernel's fixed order. */
+int oracle_prepare_view(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x,
+                        void *activation, int64_t a, int64_t b, int64_t s);
+int oracle_prepare_swiglu(const void *gate_up, int dtype, int64_t m, int64_t k, int64_t stride,
+                          void *activation);
+int oracle_norm_prepare(const void *x, int x_dtype, int64_t stride_x, const void *residual,
+                        int residual_dtype, int64_t stride_r, float *residual_out,
+                        const float *weight32, float eps, uint16_t *y, int64_t m, int64_t k,
+                        void *activation);
 
 /* Dequantize one row of k elements. Returns 0 or -1. */
 int oracle_dequantize_row(int type, const uint8_t *row, int64_t k, float *out);

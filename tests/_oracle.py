@@ -39,6 +39,17 @@ def lib():
     o.oracle_mul_mat.restype = c_int
     o.oracle_mul_mat_f32.argtypes = [c_int, ptr, i64, i64, i64, ptr, c_int, ptr, i64, c_int]
     o.oracle_mul_mat_f32.restype = c_int
+    o.oracle_float_to_bf16.argtypes = [ctypes.c_float]
+    o.oracle_float_to_bf16.restype = ctypes.c_uint16
+    o.oracle_expf.argtypes = [ctypes.c_float]
+    o.oracle_expf.restype = ctypes.c_float
+    o.oracle_prepare_view.argtypes = [ptr, c_int, i64, i64, i64, ptr, i64, i64, i64]
+    o.oracle_prepare_view.restype = c_int
+    o.oracle_prepare_swiglu.argtypes = [ptr, c_int, i64, i64, i64, ptr]
+    o.oracle_prepare_swiglu.restype = c_int
+    o.oracle_norm_prepare.argtypes = [ptr, c_int, i64, ptr, c_int, i64, ptr, ptr, ctypes.c_float, ptr, i64, i64,
+                                      ptr]
+    o.oracle_norm_prepare.restype = c_int
     o.oracle_build_info.restype = ctypes.c_char_p
     return o
 
@@ -65,6 +76,47 @@ def prepare(x, two_pass=0, dtype_code=None, stride=None):
     out = np.zeros(activation_bytes(m, k, two_pass), dtype=np.uint8)
     assert lib().oracle_prepare(_p(x), dtype_code, m, k, stride_x, _p(out), two_pass) == 0
     return out
+
+
+def _code(x):
+    return 0 if x.dtype == np.float32 else 2 if x.dtype == np.float16 else 1
+
+
+def prepare_view(x, a, b, s):
+    """Activation of x's columns permuted as [a][b][s] -> [b][a][s] (bf16 as uint16 bits)."""
+    x = np.ascontiguousarray(x)
+    m, k = x.shape
+    out = np.zeros(activation_bytes(m, k), dtype=np.uint8)
+    assert lib().oracle_prepare_view(_p(x), _code(x), m, k, k, _p(out), a, b, s) == 0
+    return out
+
+
+def prepare_swiglu(gate_up):
+    """Activation of rd(rd(silu(gate)) * up) from a merged [m, 2k] row."""
+    gate_up = np.ascontiguousarray(gate_up)
+    m, k2 = gate_up.shape
+    k = k2 // 2
+    out = np.zeros(activation_bytes(m, k), dtype=np.uint8)
+    assert lib().oracle_prepare_swiglu(_p(gate_up), _code(gate_up), m, k, k2, _p(out)) == 0
+    return out
+
+
+def norm_prepare(x, w32, eps, residual=None):
+    """-> (activation, y bf16 bits [m, k], residual_out f32 [m, k] or None)."""
+    x = np.ascontiguousarray(x)
+    m, k = x.shape
+    w32 = np.ascontiguousarray(w32, dtype=np.float32)
+    out = np.zeros(activation_bytes(m, k), dtype=np.uint8)
+    y = np.zeros((m, k), dtype=np.uint16)
+    r_out = None
+    rp, rcode = None, 0
+    if residual is not None:
+        residual = np.ascontiguousarray(residual)
+        r_out = np.zeros((m, k), dtype=np.float32)
+        rp, rcode = _p(residual), _code(residual)
+    assert lib().oracle_norm_prepare(_p(x), _code(x), k, rp, rcode, k, None if r_out is None else _p(r_out),
+                                     _p(w32), eps, _p(y), m, k, _p(out)) == 0
+    return out, y, r_out
 
 
 def split_activation(buf, m, k, two_pass=0):

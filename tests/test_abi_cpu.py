@@ -56,6 +56,35 @@ def test_bad_arguments_fail_before_any_launch(kai):
     assert kai.kai_fused_mmvq(None, 12, 16, 256, 1, dummy, 0, dummy, 0, 16, 0) == -1
 
 
+def test_producers_reject_bad_arguments_before_any_launch(kai):
+    """current_ggml_direct.cu:883-944: the reference's argument rules, checked on the host."""
+    d = ctypes.c_void_p(256)
+    assert kai.kai_fused_prepare_view(d, 1, 1, 96, 96, d, 2, 2, 32, 0) == -1      # a*b*s != k
+    assert b"Invalid fused view preparation" in kai.current_direct_error()
+    assert kai.kai_fused_prepare_view(d, 1, 9, 96, 96, d, 3, 1, 32, 0) == -1      # m > 8
+    assert kai.kai_fused_prepare_view(d, 1, 1, 96, 96, d, 6, 1, 16, 0) == -1      # s % 32
+    assert kai.kai_fused_prepare_view(d, 1, 1, 96, 64, d, 3, 1, 32, 0) == -1      # stride < k
+    assert kai.kai_fused_prepare_view(d, 3, 1, 96, 96, d, 3, 1, 32, 0) == -1      # dtype
+    assert b"F32, BF16 or F16" in kai.current_direct_error()
+    assert kai.kai_fused_prepare_view(d, 1, 1, 32800, 32800, d, 1025, 1, 32, 0) == -1
+    assert b"32768" in kai.current_direct_error()
+    assert kai.kai_fused_prepare_swiglu(d, 1, 1, 64, 127, d, 0) == -1            # stride < 2k
+    assert b"Invalid fused SwiGLU preparation" in kai.current_direct_error()
+    assert kai.kai_fused_prepare_swiglu(None, 1, 1, 64, 128, d, 0) == -1
+    assert kai.kai_fused_prepare_swiglu(d, 1, 0, 64, 128, d, 0) == -1            # m < 1
+    assert kai.kai_fused_norm_prepare(d, 1, 64, d, 0, 64, None, d, 1e-6, d, 1, 64, d, 0) == -1  # no r_out
+    assert b"Invalid fused norm preparation" in kai.current_direct_error()
+    assert kai.kai_fused_norm_prepare(d, 1, 64, None, 0, 0, None, None, 1e-6, d, 1, 64, d, 0) == -1  # no w
+    assert kai.kai_fused_norm_prepare(d, 1, 32, None, 0, 0, None, d, 1e-6, d, 1, 64, d, 0) == -1  # stride
+    assert kai.kai_fused_norm_prepare(d, 1, 64, None, 0, 0, None, d, 1e-6, ctypes.c_void_p(258), 1, 64, d,
+                                      0) == -1
+    assert b"16-byte aligned" in kai.current_direct_error()
+    assert kai.kai_fused_norm_prepare(d, 2, 64, None, 0, 0, None, d, 1e-6, d, 1, 64, d, 0) == -1  # f16 x
+    assert b"BF16 or F32" in kai.current_direct_error()
+    assert kai.kai_fused_norm_prepare(d, 1, 64, d, 2, 64, d, d, 1e-6, d, 1, 64, d, 0) == -1  # f16 residual
+    assert b"BF16 or F32" in kai.current_direct_error()
+
+
 def test_mmq_workspace_rules(kai):
     types = (ctypes.c_int * 2)(12, 14)
     rows = (ctypes.c_int64 * 2)(34816, 5120)

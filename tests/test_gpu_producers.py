@@ -1,0 +1,116 @@
+"""Fused activation producers on the GPU against the CPU oracle, through the C ABI.
+
+kai_fused_prepare_view / kai_fused_prepare_swiglu / kai_fused_norm_prepare replace the
+reference's entries of the same names (current_ggml_direct.cu:883-944). Bar: bit-exact
+activation bytes, bf16 y and fp32 residual stream; the oracle repeats the kernels' fixed
+exp and reduction order, and is pinned on the CPU (test_oracle_producers.py).
+"""
+import numpy as np
+import pytest
+import torch
+
+import _oracle as O
+from test_gpu_parity import DEV, _stream, to_dev, used_bytes
+
+pytestmark = pytest.mark.gpu
+
+CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+
+def host(t):
+    """Tensor -> numpy in the oracle's encoding (bf16 as uint16 bits)."""
+    t = t.contiguous().cpu()
+    return t.view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.bfloat16 else t.numpy()
+
+
+def act_buffer(kai, m, k):
+    return torch.full((kai.kai_fused_activation_bytes(m, k, 0),), 0xA5, dtype=torch.uint8, device=DEV)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,a,b,s,pad", [(1, 2, 3, 32, 0), (3, 16, 8, 32, 64), (8, 4, 40, 32, 0),
+                                         (2, 32, 4, 128, 32), (5, 1, 160, 32, 0)])
+def test_view_bit_exact(kai, dtype, m, a, b, s, pad):
+    k = a * b * s
+    print(f"view dtype={dtype} m={m} a={a} b={b} s={s} pad={pad}", flush=True)
+    rng = np.random.default_rng(k + m)
+    full = to_dev((rng.standard_normal((m, k + pad)) * rng.uniform(0.01, 50, (m, 1))).astype(np.float32)).to(dtype)
+    x = full[:, :k]
+    act = act_buffer(kai, m, k)
+    st = kai.kai_fused_prepare_view(x.data_ptr(), CODE[dtype], m, k, x.stride(0), act.data_ptr(), a, b, s,
+                                    _stream())
+    assert st == 0, kai.current_direct_error()
+    torch.cuda.synchronize()
+    ref = O.prepare_view(host(x), a, b, s)
+    assert np.array_equal(used_bytes(act.cpu().numpy(), m, k, 0), used_bytes(ref, m, k, 0))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,k,pad", [(1, 256, 0), (3, 5120, 64), (8, 17408, 0), (2, 32768, 0), (4, 96, 32)])
+def test_swiglu_bit_exact(kai, dtype, m, k, pad):
+    print(f"swiglu dtype={dtype} m={m} k={k} pad={pad}", flush=True)
+    rng = np.random.default_rng(k * 3 + m)
+    g = rng.standard_normal((m, k)) * 4
+    g[:, ::17] = rng.uniform(-120, 120, g[:, ::17].shape)  # exp overflow, underflow, subnormal
+    g[:, 5::31] = 0.0
+    u = rng.standard_normal((m, k))
+    full = to_dev(np.concatenate([g, u, np.zeros((m, pad))], axis=1).astype(np.float32)).to(dtype)
+    act = act_buffer(kai, m, k)
+    st = kai.kai_fused_prepare_swiglu(full.data_ptr(), CODE[dtype], m, k, full.stride(0), act.data_ptr(),
+                                      _stream())
+    assert st == 0, kai.current_direct_error()
+    torch.cuda.synchronize()
+    ref = O.prepare_swiglu(host(full[:, :2 * k]))
+    assert np.array_equal(used_bytes(act.cpu().numpy(), m, k, 0), used_bytes(ref, m, k, 0))
+
+
+@pytest.mark.parametrize("xdtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rdtype", [None, torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("m,k,pad", [(1, 96, 0), (3, 2560, 32), (8, 5120, 0), (2, 32768, 0)])
+def test_norm_bit_exact(kai, xdtype, rdtype, m, k, pad):
+    print(f"norm x={xdtype} r={rdtype} m={m} k={k} pad={pad}", flush=True)
+    rng = np.random.default_rng(k * 5 + m)
+    xs = rng.standard_normal((m, k + pad)) * rng.uniform(0.1, 30, (m, 1))
+    x = to_dev(xs.astype(np.float32)).to(xdtype)[:, :k]
+    r = None
+    if rdtype is not None:
+        r = to_dev(rng.standard_normal((m, k + pad)).astype(np.float32)).to(rdtype)[:, :k]
+    w = to_dev((1.0 + rng.standard_normal(k) * 0.2).astype(np.float32))
+    eps = 1e-6
+    y = torch.empty((m, k), dtype=torch.bfloat16, device=DEV)
+    r_out = torch.full((m, k), float("nan"), dtype=torch.float32, device=DEV) if r is not None else None
+    act = act_buffer(kai, m, k)
+    st = kai.kai_fused_norm_prepare(
+        x.data_ptr(), CODE[xdtype], x.stride(0), None if r is None else r.data_ptr(),
+        0 if r is None else CODE[rdtype], 0 if r is None else r.stride(0),
+        None if r_out is None else r_out.data_ptr(), w.data_ptr(), eps, y.data_ptr(), m, k, act.data_ptr(),
+        _stream())
+    assert st == 0, kai.current_direct_error()
+    torch.cuda.synchronize()
+    ref_act, ref_y, ref_r = O.norm_prepare(host(x), w.cpu().numpy(), eps, None if r is None else host(r))
+    assert np.array_equal(host(y), ref_y)
+    if r is not None:
+        assert np.array_equal(r_out.cpu().numpy().view(np.uint32), ref_r.view(np.uint32))
+    assert np.array_equal(used_bytes(act.cpu().numpy(), m, k, 0), used_bytes(ref_act, m, k, 0))
+
+
+def test_producer_feeds_the_gemv(kai):
+    """The SwiGLU producer's activation drives kai_fused_mmvq like kai_fused_prepare's:
+    the Q4_K down projection on it matches the oracle's GEMV on the oracle's activation."""
+    from test_gpu_parity import TOL_F32
+
+    print("swiglu -> mmvq", flush=True)
+    rng = np.random.default_rng(77)
+    m, k, n = 2, 2048, 640
+    gu = to_dev(rng.standard_normal((m, 2 * k)).astype(np.float32)).to(torch.bfloat16)
+    w = O.random_blocks(O.Q4_K, n, k, rng)
+    act = act_buffer(kai, m, k)
+    assert kai.kai_fused_prepare_swiglu(gu.data_ptr(), 1, m, k, 2 * k, act.data_ptr(), _stream()) == 0
+    w_dev = to_dev(w.reshape(n, -1))
+    out = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    st = kai.kai_fused_mmvq(w_dev.data_ptr(), O.Q4_K, n, k, m, act.data_ptr(), 0, out.data_ptr(), 0, n,
+                            _stream())
+    assert st == 0, kai.current_direct_error()
+    torch.cuda.synchronize()
+    ref = O.mul_mat(O.Q4_K, w.reshape(n, -1), k, O.prepare_swiglu(host(gu)), m)
+    assert O.normwise_rel(out.cpu().numpy(), ref) <= TOL_F32
