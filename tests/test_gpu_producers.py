@@ -114,3 +114,104 @@ def test_producer_feeds_the_gemv(kai):
     torch.cuda.synchronize()
     ref = O.mul_mat(O.Q4_K, w.reshape(n, -1), k, O.prepare_swiglu(host(gu)), m)
     assert O.normwise_rel(out.cpu().numpy(), ref) <= TOL_F32
+
+
+# ----------------------------------------------------------------- torch ops / apply()
+
+def _layer(parts_np, k, dtype=torch.bfloat16):
+    from kaillm_amd.linear import PackedGGUFLinear
+
+    layer = torch.nn.Module()
+    layer.gguf_compact = torch.nn.ModuleList([PackedGGUFLinear(to_dev(w), t, dtype) for t, w in parts_np])
+    return layer
+
+
+class _CountingLibrary:
+    """The product library with a count of kai_fused_prepare calls."""
+
+    def __init__(self, lib):
+        self._lib, self.prepares = lib, 0
+
+    def kai_fused_prepare(self, *args):
+        self.prepares += 1
+        return self._lib.kai_fused_prepare(*args)
+
+    def __getattr__(self, name):
+        return getattr(self._lib, name)
+
+
+def test_apply_swiglu_small_and_large_batches(kai):
+    from test_gpu_parity import TOL_BF16
+    from kaillm_amd.linear import GGUFLinearMethod
+
+    rng = np.random.default_rng(81)
+    k = 1024
+    parts_np = [(O.Q4_K, O.random_blocks(O.Q4_K, 256, k, rng))]
+    layer, method = _layer(parts_np, k), GGUFLinearMethod()
+
+    def act_fn(gu):
+        return torch.nn.functional.silu(gu[..., :k]) * gu[..., k:]
+
+    for m in (1, 5, 8, 12):
+        print(f"apply_swiglu m={m}", flush=True)
+        gu = to_dev(rng.standard_normal((1, m, 2 * k)).astype(np.float32)).to(torch.bfloat16)
+        y = method.apply_swiglu(layer, gu, act_fn)
+        assert y.shape == (1, m, 256) and y.dtype == torch.bfloat16
+        if m <= 8:  # the producer path
+            act = O.prepare_swiglu(host(gu.reshape(m, 2 * k)))
+        else:       # act_fn, then the batched path
+            act = O.prepare(host(act_fn(gu).reshape(m, k)), dtype_code=1)
+        ref = O.mul_mat(O.Q4_K, parts_np[0][1], k, act, m)
+        assert O.normwise_rel(y.float().reshape(m, -1).cpu().numpy(), ref) <= 2 * TOL_BF16
+
+
+def test_apply_through_input_view_equals_the_copy(kai):
+    from kaillm_amd.linear import GGUFLinearMethod
+
+    rng = np.random.default_rng(82)
+    a, b, s = 4, 8, 64
+    k = a * b * s
+    parts_np = [(O.Q6_K, O.random_blocks(O.Q6_K, 192, k, rng)), (O.Q4_K, O.random_blocks(O.Q4_K, 64, k, rng))]
+    layer, method = _layer(parts_np, k), GGUFLinearMethod()
+    layer._kai_input_gather = torch.arange(k, device=DEV).reshape(a, b, s).transpose(0, 1).reshape(k)
+    layer._kai_input_view = (a, b, s)
+    plain = _layer(parts_np, k)
+    for m in (1, 3, 8, 16):
+        print(f"apply view m={m}", flush=True)
+        x = to_dev(rng.standard_normal((m, k)).astype(np.float32)).to(torch.bfloat16)
+        got = method.apply(layer, x)
+        want = GGUFLinearMethod().apply(plain, x[:, layer._kai_input_gather].contiguous())
+        assert torch.equal(got, want)
+
+
+def test_norm_prepare_stash_feeds_its_consumer(kai, monkeypatch):
+    from test_gpu_parity import TOL_F32
+    from kaillm_amd import native_fused
+    from kaillm_amd.linear import GGUFLinearMethod
+
+    rng = np.random.default_rng(83)
+    m, k, eps = 3, 2048, 1e-6
+    parts_np = [(O.Q4_K, O.random_blocks(O.Q4_K, 320, k, rng))]
+    layer, method = _layer(parts_np, k, torch.float32), GGUFLinearMethod()
+    producer = 12345
+    layer._kai_act_producer = producer
+    counting = _CountingLibrary(native_fused.library())
+    monkeypatch.setattr(native_fused, "library", lambda: counting)
+    monkeypatch.setattr(native_fused, "CONSUMER_OF", {})
+    monkeypatch.setattr(native_fused, "STASH", {})
+    method._fused(layer)
+    assert native_fused.CONSUMER_OF == {layer._kai_fused.weights[0].data_ptr(): producer}
+
+    x = to_dev(rng.standard_normal((m, k)).astype(np.float32)).to(torch.bfloat16)
+    r = to_dev(rng.standard_normal((m, k)).astype(np.float32))
+    w32 = to_dev((1 + 0.1 * rng.standard_normal(k)).astype(np.float32))
+    y, r_out = native_fused.norm_prepare(producer, x, r, w32, eps)
+    ref_act, ref_y, ref_r = O.norm_prepare(host(x), w32.cpu().numpy(), eps, r.cpu().numpy())
+    assert np.array_equal(host(y), ref_y) and np.array_equal(r_out.cpu().numpy(), ref_r)
+    out = method.apply(layer, y)
+    assert counting.prepares == 0                      # the stashed activation was used
+    ref = O.mul_mat(O.Q4_K, parts_np[0][1], k, ref_act, m)
+    assert O.normwise_rel(out.cpu().numpy(), ref) <= TOL_F32
+    method.apply(layer, y.clone())                     # another tensor: prepares its own
+    assert counting.prepares == 1
+    assert native_fused.norm_prepare(producer, x.float().to(torch.float16), None, w32, eps) is None  # F16 x
