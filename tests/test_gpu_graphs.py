@@ -1,0 +1,92 @@
+"""Projection groups captured in a HIP graph (torch.cuda.CUDAGraph) replay exactly as they run eagerly.
+
+A decode step of the fused path — the Gemma norm producer feeding a merged Q4_K/Q6_K
+projection, a SwiGLU down projection and a projection read through an input view — and
+the batched path (fp16-MFMA and int8 MMQ kernels with their scratch) are captured once,
+then replayed with new inputs written into the captured buffers. Between replays the same
+step runs eagerly on the same inputs, and every replay must equal it bit for bit (the
+kernels have fixed reduction orders and no atomics). The library issues no memset and no
+allocation of its own; torch's graph pool holds every buffer.
+"""
+import numpy as np
+import pytest
+import torch
+
+import _oracle as O
+from test_gpu_parity import DEV, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _layer(parts_np, dtype=torch.bfloat16):
+    from kaillm_amd.linear import PackedGGUFLinear
+
+    layer = torch.nn.Module()
+    layer.gguf_compact = torch.nn.ModuleList([PackedGGUFLinear(to_dev(w), t, dtype) for t, w in parts_np])
+    return layer
+
+
+@pytest.mark.parametrize("m", [1, 4, 8, 16, 64])
+def test_decode_step_graph_replays_equal_eager(kai, m, monkeypatch):
+    from kaillm_amd import native_fused
+    from kaillm_amd.linear import GGUFLinearMethod
+
+    print(f"graph step m={m}", flush=True)
+    monkeypatch.setattr(native_fused, "CONSUMER_OF", {})
+    monkeypatch.setattr(native_fused, "STASH", {})
+    rng = np.random.default_rng(900 + m)
+    k, kf = 2048, 1536
+    a, b, s = 4, 8, 64
+    method = GGUFLinearMethod()
+    qkv = _layer([(O.Q4_K, O.random_blocks(O.Q4_K, 384, k, rng)), (O.Q6_K, O.random_blocks(O.Q6_K, 128, k, rng))])
+    producer = 4242
+    qkv._kai_act_producer = producer
+    down = _layer([(O.Q6_K, O.random_blocks(O.Q6_K, 256, kf, rng))])
+    viewed = _layer([(O.Q4_K, O.random_blocks(O.Q4_K, 256, k, rng))])
+    viewed._kai_input_gather = torch.arange(k, device=DEV).reshape(a, b, s).transpose(0, 1).reshape(k)
+    viewed._kai_input_view = (a, b, s)
+    w32 = to_dev((1 + 0.1 * rng.standard_normal(k)).astype(np.float32))
+
+    x = torch.empty((m, k), dtype=torch.bfloat16, device=DEV)
+    res = torch.empty((m, k), dtype=torch.float32, device=DEV)
+    gu = torch.empty((m, 2 * kf), dtype=torch.bfloat16, device=DEV)
+    xv = torch.empty((m, k), dtype=torch.bfloat16, device=DEV)
+
+    def act_fn(t):
+        return torch.nn.functional.silu(t[..., :kf]) * t[..., kf:]
+
+    def step():
+        fused = native_fused.norm_prepare(producer, x, res, w32, 1e-6) if m <= 8 else None
+        y, r_out = fused if fused is not None else (x, res)
+        return [method.apply(qkv, y), method.apply_swiglu(down, gu, act_fn), method.apply(viewed, xv), r_out]
+
+    def fill(seed):
+        g = np.random.default_rng(seed)
+        x.copy_(to_dev(g.standard_normal((m, k)).astype(np.float32)).to(torch.bfloat16))
+        res.copy_(to_dev(g.standard_normal((m, k)).astype(np.float32)))
+        gu.copy_(to_dev(g.standard_normal((m, 2 * kf)).astype(np.float32)).to(torch.bfloat16))
+        xv.copy_(to_dev(g.standard_normal((m, k)).astype(np.float32)).to(torch.bfloat16))
+
+    fill(1)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out = step()
+    torch.cuda.synchronize()
+    if m <= 8:
+        assert native_fused.CONSUMER_OF  # the qkv consumer was registered for the producer
+    for replay in range(3):
+        fill(10 + replay)
+        eager = [t.clone() for t in step()]
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, want in zip(static_out, eager):
+            assert torch.equal(got, want), f"replay {replay}"
+    del graph
