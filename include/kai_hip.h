@@ -73,6 +73,14 @@ int kai_fused_norm_prepare(const void *x, int x_dtype, int64_t stride_x, const v
                            const float *weight32, float eps, void *y, int64_t m, int64_t k,
                            void *activation, uintptr_t stream);
 
+/* Dequantise `rows` contiguous rows of `cols` values (GGUF wire bytes, cols a multiple of
+ * the block size) to out [rows, cols] as F32 (0), BF16 (1) or F16 (2), out 16-byte aligned.
+ * Each value is the format's formula in fp32 (gguf-py quants.py order, no fused
+ * multiply-add), rounded to nearest even. Replaces the torch op ggml_dequantize
+ * (csrc/gguf/gguf_kernel.cu:87-102), which has no C entry point in the reference. */
+int kai_dequantize(const void *weight, int type, int64_t rows, int64_t cols, void *out, int out_dtype,
+                   uintptr_t stream);
+
 /* GEMV: dst[j * stride_dst + r] = inverse[j] * sum_b dot(W[r, b], q8[j, b]) for
  * r < n, j < m <= 8; F32 or BF16 (dst_bf16) output.
  * Replaces kai_fused_mmvq (current_ggml_direct.cu:946-965; kernel kai_dual_mmvq.cuh:258-397). */

@@ -161,6 +161,19 @@ extern "C" int kai_fused_norm_prepare(const void *x, int x_dtype, int64_t stride
     });
 }
 
+extern "C" int kai_dequantize(const void *weight, int type, int64_t rows, int64_t cols, void *out, int out_dtype,
+                              uintptr_t stream) {
+    return entry([&] {
+        const int qk = kai::block_elems(type);
+        if (!kai::weight_type_supported(type)) throw kai::Error("Unsupported GGML weight type");
+        if (rows < 0 || cols <= 0 || cols % qk || (rows > 0 && (!weight || !out)) ||
+            (rows > 0 && cols > INT64_MAX / rows))
+            throw kai::Error("Invalid dequantization arguments");
+        if (reinterpret_cast<uintptr_t>(out) % 16) throw kai::Error("Dequantized output must be 16-byte aligned");
+        kai::launch_dequantize(weight, type, rows * cols, out, out_dtype, stream_of(stream));
+    });
+}
+
 extern "C" int kai_fused_mmvq(const void *weight, int type, int64_t n, int64_t k, int64_t m,
                               const void *activation, int two_pass, void *dst, int dst_bf16, int64_t stride_dst,
                               uintptr_t stream) {

@@ -45,6 +45,10 @@ inline ActLayout activation_layout(void *activation, int64_t m, int64_t k, int t
             reinterpret_cast<float *>(base + pass * (two_pass ? 2 : 1))};
 }
 
+// `values` weight values (a whole number of blocks, rows back to back) to F32 (0), BF16 (1)
+// or F16 (2) in row-major order.
+void launch_dequantize(const void *w, int type, int64_t values, void *out, int out_dtype, hipStream_t stream);
+
 void launch_prepare(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const ActLayout &out,
                     hipStream_t stream);
 // Fused producers of the single-pass activation (kai_prepare.hip): x[..., view], silu(gate)

@@ -85,6 +85,20 @@ def test_producers_reject_bad_arguments_before_any_launch(kai):
     assert b"BF16 or F32" in kai.current_direct_error()
 
 
+def test_dequantize_rejects_bad_arguments_before_any_launch(kai):
+    d = ctypes.c_void_p(256)
+    assert kai.kai_dequantize(d, 3, 4, 256, d, 1, 0) == -1           # Q4_1 is not implemented
+    assert b"Unsupported GGML weight type" in kai.current_direct_error()
+    assert kai.kai_dequantize(d, 12, 4, 288, d, 1, 0) == -1          # cols % 256
+    assert b"Invalid dequantization" in kai.current_direct_error()
+    assert kai.kai_dequantize(None, 12, 4, 256, d, 1, 0) == -1
+    assert kai.kai_dequantize(d, 12, -1, 256, d, 1, 0) == -1
+    assert kai.kai_dequantize(d, 8, 4, 64, ctypes.c_void_p(258), 2, 0) == -1
+    assert b"16-byte aligned" in kai.current_direct_error()
+    assert kai.kai_dequantize(d, 8, 4, 64, d, 3, 0) == -1            # output dtype
+    assert b"F32, BF16 or F16" in kai.current_direct_error()
+
+
 def test_mmq_workspace_rules(kai):
     types = (ctypes.c_int * 2)(12, 14)
     rows = (ctypes.c_int64 * 2)(34816, 5120)
