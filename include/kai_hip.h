@@ -81,6 +81,19 @@ int kai_fused_norm_prepare(const void *x, int x_dtype, int64_t stride_x, const v
 int kai_dequantize(const void *weight, int type, int64_t rows, int64_t cols, void *out, int out_dtype,
                    uintptr_t stream);
 
+/* Copy a GGUF tensor's rows from the model file at `path` into device memory, bytes
+ * unchanged: the tensor starts at file_offset and holds src_rows rows of row_bytes. dst row r
+ * (r < rows) receives source row row_order[r] (row_order NULL: row r); with block_order,
+ * block j (block_bytes each) of every dst row receives the source row's block block_order[j].
+ * Reads go through pinned staging buffers and hipMemcpyAsync on `stream`; returns when the
+ * copies are complete. Replaces the reference's read-then-permute of stored tensors
+ * (gguf-reader/gguf/gguf_reader.py:116-390 memory-mapped reads, then
+ * quantization/yaqa_linear.py:102-127 _permute_stored on the host copy), which has no C entry
+ * point in the reference. */
+int kai_upload_rows(const char *path, int64_t file_offset, int64_t src_rows, int64_t row_bytes,
+                    const int64_t *row_order, int64_t rows, int64_t block_bytes,
+                    const int64_t *block_order, void *dst, uintptr_t stream);
+
 /* GEMV: dst[j * stride_dst + r] = inverse[j] * sum_b dot(W[r, b], q8[j, b]) for
  * r < n, j < m <= 8; F32 or BF16 (dst_bf16) output.
  * Replaces kai_fused_mmvq (current_ggml_direct.cu:946-965; kernel kai_dual_mmvq.cuh:258-397). */

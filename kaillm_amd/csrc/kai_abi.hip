@@ -174,6 +174,18 @@ extern "C" int kai_dequantize(const void *weight, int type, int64_t rows, int64_
     });
 }
 
+extern "C" int kai_upload_rows(const char *path, int64_t file_offset, int64_t src_rows, int64_t row_bytes,
+                               const int64_t *row_order, int64_t rows, int64_t block_bytes,
+                               const int64_t *block_order, void *dst, uintptr_t stream) {
+    return entry([&] {
+        if (!path || file_offset < 0 || src_rows < 0 || row_bytes <= 0 || rows < 0 || (rows > 0 && !dst) ||
+            (!row_order && rows > src_rows) || (block_order && (block_bytes <= 0 || row_bytes % block_bytes)))
+            throw kai::Error("Invalid upload arguments");
+        kai::upload_rows(path, file_offset, src_rows, row_bytes, row_order, rows, block_bytes, block_order, dst,
+                         stream_of(stream));
+    });
+}
+
 extern "C" int kai_fused_mmvq(const void *weight, int type, int64_t n, int64_t k, int64_t m,
                               const void *activation, int two_pass, void *dst, int dst_bf16, int64_t stride_dst,
                               uintptr_t stream) {

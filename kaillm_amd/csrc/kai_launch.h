@@ -45,6 +45,12 @@ inline ActLayout activation_layout(void *activation, int64_t m, int64_t k, int t
             reinterpret_cast<float *>(base + pass * (two_pass ? 2 : 1))};
 }
 
+// Destination row r of dst = source row row_order[r] (or r) of the tensor at file_offset of
+// the file at path, with destination block j = source block block_order[j] (or j) within
+// each row; returns once the copies on `stream` have completed.
+void upload_rows(const char *path, int64_t file_offset, int64_t src_rows, int64_t row_bytes, const int64_t *row_order,
+                 int64_t rows, int64_t block_bytes, const int64_t *block_order, void *dst, hipStream_t stream);
+
 // `values` weight values (a whole number of blocks, rows back to back) to F32 (0), BF16 (1)
 // or F16 (2) in row-major order.
 void launch_dequantize(const void *w, int type, int64_t values, void *out, int out_dtype, hipStream_t stream);
