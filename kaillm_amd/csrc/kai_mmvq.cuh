@@ -4,7 +4,8 @@
 // Reference: kai_dual::mmvq_dual (vllm_gguf_plugin/native/kernels/kai_dual_mmvq.cuh:258-327)
 // and its launcher (:329-397). Design for gfx950 instead of warp32 CTAs:
 //   * a wave64 works on 64/G rows at once, one group of G lanes per row (G = 16..64,
-//     wider for long rows, pick_group);
+//     wider for long rows, pick_group), and on RS such row sets one after the other
+//     (gemv_row_sets);
 //     the lanes of a group walk the row's ~32-byte units (kai_units.h) in order, so
 //     each load instruction reads contiguous runs of G units of wire bytes;
 //   * a ring of DEPTH units per lane of wire bytes is kept in flight: unit t + DEPTH is
@@ -60,7 +61,7 @@ inline size_t mmvq_act_lds_bytes(int64_t m, int64_t k, bool two_pass) {
 
 template <int M> constexpr int mmvq_threads() { return M <= 4 ? 256 : 128; }
 
-template <int TYPE, int M, bool TWO_PASS, int DEPTH, int G>
+template <int TYPE, int M, bool TWO_PASS, int DEPTH, int G, int RS>
 __global__ __launch_bounds__(mmvq_threads<M>())
 void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrows, int units_per_row,
                  const block_q8_1 *__restrict__ y1, const block_q8_1 *__restrict__ y2, int y_row_blocks,
@@ -76,23 +77,29 @@ void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrow
 
     const int lane = threadIdx.x % WAVE;
     const int gpos = lane % G;
-    const int row = (blockIdx.x * (THREADS / WAVE) + threadIdx.x / WAVE) * (WAVE / G) + lane / G;
+    // A wave owns RS row sets of WAVE / G consecutive rows, one group of G lanes per row,
+    // streamed one after the other with the load ring running across their boundaries.
+    const int wave_row0 = (blockIdx.x * (THREADS / WAVE) + threadIdx.x / WAVE) * (WAVE / G) * RS;
+    auto row_of = [&](int rs) { return wave_row0 + rs * (WAVE / G) + lane / G; };
     const int nb = y_row_blocks;
     const U unit = make_unit<TYPE>(gpos % U::PER_BLOCK, grid_lds);
-    const uint8_t *wrow = weight + static_cast<int64_t>(min(row, nrows - 1)) * row_bytes;
     const int T = (units_per_row + G - 1) / G;
 
     // Prime the ring first so the staging below overlaps the HBM latency. Every load is
-    // unconditional (unit indices are clamped to the row; clamped units contribute zero),
-    // so the compiler's vmcnt waits are exact and DEPTH units per lane stay in flight.
+    // unconditional (unit indices are clamped to the row, rows to the matrix, row sets to
+    // the wave's; clamped units contribute zero), so the compiler's vmcnt waits are exact
+    // and DEPTH units per lane stay in flight. Step t of a lane is unit gpos + G (t % T)
+    // of row set t / T.
     const int last = units_per_row - 1;
-    auto load_unit = [&](typename U::W &w, int u) {
+    auto load_unit = [&](typename U::W &w, int t) {
+        const int rs = t / T, u = gpos + G * (t - rs * T);
+        const uint8_t *wrow = weight + static_cast<int64_t>(min(row_of(min(rs, RS - 1)), nrows - 1)) * row_bytes;
         unit.load_w(w, wrow + static_cast<int64_t>(min(u, last) / U::PER_BLOCK) * BYTES);
     };
     typename U::W ring[DEPTH];
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
-        load_unit(ring[d], gpos + G * d);
+        load_unit(ring[d], d);
         __asm__ volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -128,7 +135,7 @@ void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrow
         }
         __syncthreads();
     }
-    if (row - lane / G >= nrows) return;  // whole wave past the last row
+    if (wave_row0 >= nrows) return;  // whole wave past the last row
 
     float acc[M];
 #pragma unroll
@@ -137,15 +144,16 @@ void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrow
     // T >= 1; a do-while keeps the prologue loads from being sunk behind a zero-trip check.
     // The memory clobbers keep each unit's loads where they are issued and the scheduling
     // barriers keep the next unit's arithmetic (and its load waits) out of this one.
-    const int TT = (T + DEPTH - 1) / DEPTH * DEPTH;
+    const int TT = (RS * T + DEPTH - 1) / DEPTH * DEPTH;
     int t0 = 0;
     do {
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
-            const int u = gpos + G * (t0 + d);
-            const bool live = u < units_per_row;  // false for every unit past the row end
+            const int t = t0 + d, rs = t / T, tu = t - rs * T;
+            const int u = gpos + G * tu;
+            const bool live = u < units_per_row && rs < RS;  // false past the row end and the last set
             const typename U::P w = unit.prep(ring[d]);
-            load_unit(ring[d], u + G * DEPTH);
+            load_unit(ring[d], t + DEPTH);
             const int blk = min(u, last) / U::PER_BLOCK;
 #pragma unroll
             for (int j = 0; j < M; ++j) {
@@ -158,13 +166,24 @@ void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrow
                     acc[j] += live ? v : 0.0f;
                 }
             }
+            if (RS > 1 && tu == T - 1 && rs < RS - 1) {  // row set rs complete (uniform); the last below
+#pragma unroll
+                for (int j = 0; j < M; ++j) {
+                    const float total = group_sum<G>(acc[j]);
+                    if (gpos == j % G && row_of(rs) < nrows)
+                        store_out(dst, dst_bf16 != 0, static_cast<int64_t>(j) * stride_dst + row_of(rs), total * inv_lds[j]);
+                    acc[j] = 0.0f;
+                }
+            }
             __asm__ volatile("" ::: "memory");
             __builtin_amdgcn_sched_barrier(0);
         }
         t0 += DEPTH;
     } while (t0 < TT);
 
-    // Group totals; lane gpos of a group stores activation rows j = gpos, gpos + G, ...
+    // Group totals of the last row set; lane gpos of a group stores activation rows
+    // j = gpos, gpos + G, ...
+    const int row = row_of(RS - 1);
 #pragma unroll
     for (int j = 0; j < M; ++j) {
         const float total = group_sum<G>(acc[j]);
@@ -173,20 +192,31 @@ void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrow
     }
 }
 
-template <int TYPE, int M, bool TWO_PASS, int G>
-static void launch_variant(const uint8_t *w, int64_t n, int64_t k, const block_q8_1 *y1, const block_q8_1 *y2,
-                           const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
+// Row sets per wave: two for one or two activation rows when the matrix still gives at
+// least 4096 waves (four per SIMD of a 256-CU device) after pairing its row sets; the
+// second set's loads then overlap the first set's reduction and the activation is staged
+// once per twice the weight bytes. Measured on MI355X: Q4_K gate/up 34816 x 5120 -11 %
+// at one row, -9 % at two; smaller matrices lose parallelism and stay at one set.
+template <int M>
+inline int gemv_row_sets(int64_t n, int g) {
+    const int64_t sets = (n + (WAVE / g) - 1) / (WAVE / g);
+    return M <= 2 && sets >= 2 * 4096 ? 2 : 1;
+}
+
+template <int TYPE, int M, bool TWO_PASS, int G, int RS>
+static void launch_sets(const uint8_t *w, int64_t n, int64_t k, const block_q8_1 *y1, const block_q8_1 *y2,
+                        const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
     constexpr int THREADS = mmvq_threads<M>();
     constexpr int DEPTH = M <= 2 ? 3 : 2;
     constexpr int QK = block_elems(TYPE);
     const int64_t blocks_per_row = k / QK;
     const int64_t row_bytes = blocks_per_row * block_bytes(TYPE);
     const int units = static_cast<int>(blocks_per_row * Unit<TYPE>::PER_BLOCK);
-    const int64_t rows_per_block = (THREADS / WAVE) * (WAVE / G);
+    const int64_t rows_per_block = (THREADS / WAVE) * (WAVE / G) * RS;
     const size_t lds = mmvq_act_lds_bytes(M, k, TWO_PASS);
     if (lds + (TYPE == IQ3_S ? 2048 : 0) + 64 > size_t(MMVQ_LDS_BUDGET))
         throw Error("GEMV activation does not fit in LDS (m * k too large)");
-    auto kernel = mmvq_kernel<TYPE, M, TWO_PASS, DEPTH, G>;
+    auto kernel = mmvq_kernel<TYPE, M, TWO_PASS, DEPTH, G, RS>;
     static bool attribute_set = false;  // per instantiation; raises the dynamic LDS limit once
     if (!attribute_set) {
         if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -197,6 +227,18 @@ static void launch_variant(const uint8_t *w, int64_t n, int64_t k, const block_q
     kernel<<<dim3(static_cast<unsigned>((n + rows_per_block - 1) / rows_per_block)), dim3(THREADS), lds, stream>>>(
         w, row_bytes, static_cast<int>(n), units, y1, y2, static_cast<int>(k / QK8_1), inverse, dst, stride_dst,
         dst_bf16 ? 1 : 0);
+}
+
+template <int TYPE, int M, bool TWO_PASS, int G>
+static void launch_variant(const uint8_t *w, int64_t n, int64_t k, const block_q8_1 *y1, const block_q8_1 *y2,
+                           const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
+    if constexpr (M <= 2) {
+        if (gemv_row_sets<M>(n, G) == 2) {
+            launch_sets<TYPE, M, TWO_PASS, G, 2>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream);
+            return;
+        }
+    }
+    launch_sets<TYPE, M, TWO_PASS, G, 1>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream);
 }
 
 // Lanes per row: 16, doubled while a row would leave more than 8 units per lane. A
