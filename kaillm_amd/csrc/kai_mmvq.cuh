@@ -86,13 +86,14 @@ void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrow
     const int T = (units_per_row + G - 1) / G;
 
     // Prime the ring first so the staging below overlaps the HBM latency. Every load is
-    // unconditional (unit indices are clamped to the row, rows to the matrix, row sets to
-    // the wave's; clamped units contribute zero), so the compiler's vmcnt waits are exact
-    // and DEPTH units per lane stay in flight. Step t of a lane is unit gpos + G (t % T)
-    // of row set t / T.
+    // unconditional (unit indices are clamped to the row, rows to the matrix, steps past
+    // the last row set to its last unit; clamped units contribute zero), so the compiler's
+    // vmcnt waits are exact and DEPTH units per lane stay in flight. Step t of a lane is
+    // unit gpos + G (t % T) of row set t / T.
     const int last = units_per_row - 1;
     auto load_unit = [&](typename U::W &w, int t) {
-        const int rs = t / T, u = gpos + G * (t - rs * T);
+        // Past the wave's last set: re-read the last unit of the last row (still cached).
+        const int rs = t / T, u = rs >= RS ? last : gpos + G * (t - rs * T);
         const uint8_t *wrow = weight + static_cast<int64_t>(min(row_of(min(rs, RS - 1)), nrows - 1)) * row_bytes;
         unit.load_w(w, wrow + static_cast<int64_t>(min(u, last) / U::PER_BLOCK) * BYTES);
     };
