@@ -89,18 +89,27 @@ void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrow
     // unconditional (unit indices are clamped to the row, rows to the matrix, steps past
     // the last row set to its last unit; clamped units contribute zero), so the compiler's
     // vmcnt waits are exact and DEPTH units per lane stay in flight. Step t of a lane is
-    // unit gpos + G (t % T) of row set t / T.
+    // unit gpos + G (t % T) of row set t / T, tracked by counters.
     const int last = units_per_row - 1;
-    auto load_unit = [&](typename U::W &w, int t) {
+    // Step positions (row set, step within the set) advance by one per unit, uniformly.
+    auto advance = [&](int &rs, int &tu) {
+        if (++tu == T) {
+            tu = 0;
+            ++rs;
+        }
+    };
+    auto load_unit = [&](typename U::W &w, int rs, int tu) {
         // Past the wave's last set: re-read the last unit of the last row (still cached).
-        const int rs = t / T, u = rs >= RS ? last : gpos + G * (t - rs * T);
+        const int u = rs >= RS ? last : gpos + G * tu;
         const uint8_t *wrow = weight + static_cast<int64_t>(min(row_of(min(rs, RS - 1)), nrows - 1)) * row_bytes;
         unit.load_w(w, wrow + static_cast<int64_t>(min(u, last) / U::PER_BLOCK) * BYTES);
     };
     typename U::W ring[DEPTH];
+    int lrs = 0, ltu = 0;  // position of the next load
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
-        load_unit(ring[d], d);
+        load_unit(ring[d], lrs, ltu);
+        advance(lrs, ltu);
         __asm__ volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -146,15 +155,15 @@ void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrow
     // The memory clobbers keep each unit's loads where they are issued and the scheduling
     // barriers keep the next unit's arithmetic (and its load waits) out of this one.
     const int TT = (RS * T + DEPTH - 1) / DEPTH * DEPTH;
-    int t0 = 0;
+    int t0 = 0, rs = 0, tu = 0;  // position of the unit being multiplied
     do {
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
-            const int t = t0 + d, rs = t / T, tu = t - rs * T;
             const int u = gpos + G * tu;
             const bool live = u < units_per_row && rs < RS;  // false past the row end and the last set
             const typename U::P w = unit.prep(ring[d]);
-            load_unit(ring[d], t + DEPTH);
+            load_unit(ring[d], lrs, ltu);
+            advance(lrs, ltu);
             const int blk = min(u, last) / U::PER_BLOCK;
 #pragma unroll
             for (int j = 0; j < M; ++j) {
@@ -176,6 +185,7 @@ void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrow
                     acc[j] = 0.0f;
                 }
             }
+            advance(rs, tu);
             __asm__ volatile("" ::: "memory");
             __builtin_amdgcn_sched_barrier(0);
         }
