@@ -203,16 +203,18 @@ void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrow
     }
 }
 
-// Row sets per wave: two for up to four activation rows when the matrix still gives at
-// least 4096 waves (four per SIMD of a 256-CU device) after pairing its row sets; the
-// second set's loads then overlap the first set's reduction and the activation is staged
-// once per twice the weight bytes. Measured on MI355X: Q4_K gate/up 34816 x 5120 -11 %,
-// -9 %, -14 %, -18 % at one to four rows; smaller matrices lose parallelism and stay at
-// one set.
-template <int M>
+// Row sets per wave: two when the matrix still gives at least 4096 waves (four per SIMD
+// of a 256-CU device) after pairing its row sets, for Q4_K at one to four activation rows
+// and for the other formats at three or four; the second set's loads then overlap the
+// first set's reduction and the activation is staged once per twice the weight bytes.
+// Measured on MI355X, 34816 x 5120: Q4_K -11 %, -9 %, -14 %, -18 % at one to four rows;
+// Q2_K and IQ3_S -10 % to -22 % at three and four rows but +5 % at one; smaller matrices
+// lose parallelism and stay at one set.
+template <int TYPE, int M>
 inline int gemv_row_sets(int64_t n, int g) {
     const int64_t sets = (n + (WAVE / g) - 1) / (WAVE / g);
-    return M <= 4 && sets >= 2 * 4096 ? 2 : 1;
+    const bool rows_ok = TYPE == Q4_K ? M <= 4 : (M >= 3 && M <= 4);
+    return rows_ok && sets >= 2 * 4096 ? 2 : 1;
 }
 
 template <int TYPE, int M, bool TWO_PASS, int G, int RS>
@@ -245,7 +247,7 @@ template <int TYPE, int M, bool TWO_PASS, int G>
 static void launch_variant(const uint8_t *w, int64_t n, int64_t k, const block_q8_1 *y1, const block_q8_1 *y2,
                            const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
     if constexpr (M <= 4) {
-        if (gemv_row_sets<M>(n, G) == 2) {
+        if (gemv_row_sets<TYPE, M>(n, G) == 2) {
             launch_sets<TYPE, M, TWO_PASS, G, 2>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream);
             return;
         }
