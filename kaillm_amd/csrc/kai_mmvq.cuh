@@ -221,7 +221,9 @@ template <int TYPE, int M, bool TWO_PASS, int G, int RS>
 static void launch_sets(const uint8_t *w, int64_t n, int64_t k, const block_q8_1 *y1, const block_q8_1 *y2,
                         const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
     constexpr int THREADS = mmvq_threads<M>();
-    constexpr int DEPTH = M <= 2 ? 3 : 2;
+    // ring depth: 3 units for one or two rows on one row set; with two sets (and from three
+    // rows on) 2, which keeps more waves resident
+    constexpr int DEPTH = M <= 2 && RS == 1 ? 3 : 2;
     constexpr int QK = block_elems(TYPE);
     const int64_t blocks_per_row = k / QK;
     const int64_t row_bytes = blocks_per_row * block_bytes(TYPE);
