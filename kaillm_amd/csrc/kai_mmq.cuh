@@ -302,8 +302,9 @@ static void launch_mmq_tile(const void *weight, int64_t n, int64_t k, const bloc
     constexpr int MT = 16 * TM, ROWS = 16 * TN * (4 / KS);
     const int64_t row_bytes = (k / block_elems(TYPE)) * block_bytes(TYPE);
     const size_t lds = mmq_lds_bytes<TYPE, TM, TN, KS>();
-    // weight steps in flight: deeper when the per-step work is short
-    constexpr int DEPTH = TM <= 2 ? 4 : 2;
+    // weight steps in flight: two (a deeper ring costs resident waves; measured on MI355X
+    // at 8-16 rows: Q4_K gate/up -4 %, Q6_K down -3..-5 % against four)
+    constexpr int DEPTH = 2;
     auto kernel = mmq_kernel<TYPE, TM, TN, KS, DEPTH>;
     static bool attribute_set = false;
     if (!attribute_set) {
