@@ -93,18 +93,27 @@ __device__ __forceinline__ float quad_sum(float v) {
 }
 
 // Scale of a row from its maximum |x|, read by every workgroup of the row.
+// The row is read in runs of 8 values, run p by thread p % PREP_THREADS; the run this
+// workgroup's thread quantises (blockIdx.y * PREP_THREADS + threadIdx.x: 4 lanes per
+// block, PREP_BLOCKS blocks per workgroup) is kept in `own`, so the values are read once.
 template <int DTYPE>
 __device__ __forceinline__ float row_scale(const typename Src<DTYPE>::T *xr, int k, float *lds, float *inverse_out,
-                                           bool writer) {
+                                           bool writer, float (&own)[8]) {
     float mx = 0.0f;
-    for (int p = threadIdx.x; p < k / 8; p += PREP_THREADS) {
+    int i = 0;
+    for (int p = threadIdx.x; p < k / 8; p += PREP_THREADS, ++i) {
         float v[8];
         load8<DTYPE>(xr + 8 * p, v);
 #pragma unroll
         for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[j]));
+        if (i == int(blockIdx.y)) {  // uniform
+#pragma unroll
+            for (int j = 0; j < 8; ++j) own[j] = v[j];
+        }
     }
     return row_scale_from_max(block_max(mx, lds), inverse_out, writer);
 }
+static_assert(PREP_THREADS == 4 * PREP_BLOCKS, "one run of 8 values per thread and workgroup");
 
 // Codes of the lane's 8 values of one block: d = max|v| / 127 over the block (quad),
 // q = roundf(v / d); returns the fp32 d, the stored fp16 bits and the block's code sum.
@@ -154,10 +163,9 @@ __global__ __launch_bounds__(PREP_THREADS) void prepare_q8_1_kernel(
     const int nblocks = k / QK8_1;
     const int part = threadIdx.x & 3, ib = blockIdx.y * PREP_BLOCKS + (threadIdx.x >> 2);
     const auto *xr = x + static_cast<int64_t>(row) * stride_x;
-    const float scale = row_scale<DTYPE>(xr, k, wave_max_lds, inverse + row, blockIdx.y == 0 && threadIdx.x == 0);
-    if (ib >= nblocks) return;  // whole quads
     float v[8];
-    load8<DTYPE>(xr + ib * QK8_1 + 8 * part, v);
+    const float scale = row_scale<DTYPE>(xr, k, wave_max_lds, inverse + row, blockIdx.y == 0 && threadIdx.x == 0, v);
+    if (ib >= nblocks) return;  // whole quads
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] *= scale;
     int8_t q1[8];
@@ -207,10 +215,9 @@ __global__ __launch_bounds__(PREP_THREADS) void prepare_mmf_kernel(
     const int nblocks = k / QK8_1;
     const int part = threadIdx.x & 3, ib = blockIdx.y * PREP_BLOCKS + (threadIdx.x >> 2);
     const auto *xr = x + static_cast<int64_t>(row) * stride_x;
-    const float scale = row_scale<DTYPE>(xr, k, wave_max_lds, inverse + row, blockIdx.y == 0 && threadIdx.x == 0);
-    if (ib >= nblocks) return;  // whole quads
     float v[8];
-    load8<DTYPE>(xr + ib * QK8_1 + 8 * part, v);
+    const float scale = row_scale<DTYPE>(xr, k, wave_max_lds, inverse + row, blockIdx.y == 0 && threadIdx.x == 0, v);
+    if (ib >= nblocks) return;  // whole quads
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] *= scale;
     int8_t q[8];
