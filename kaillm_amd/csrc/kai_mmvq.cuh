@@ -59,15 +59,22 @@ inline size_t mmvq_act_lds_bytes(int64_t m, int64_t k, bool two_pass) {
     return size_t(two_pass ? 2 : 1) * size_t(m) * size_t(k / QK8_1) * 40;
 }
 
-template <int M> constexpr int mmvq_threads() { return M <= 4 ? 256 : 128; }
+// Threads per workgroup, measured on MI355X: 512 on one row set when the activation
+// staging is shared by more rows without leaving too few workgroups (short rows, G <= 16:
+// qkv / o_proj -2..-7 %; or three and four rows: 5120 x 17408 down -13..-16 %); 256
+// otherwise (two row sets: gate/up -8 % against 512; long rows at one or two activation
+// rows: down +10..17 % at 512); 128 from five rows on.
+template <int M, int RS, int G> constexpr int mmvq_threads() {
+    return M > 4 ? 128 : (RS == 1 && (G <= 16 || M >= 3)) ? 512 : 256;
+}
 
 template <int TYPE, int M, bool TWO_PASS, int DEPTH, int G, int RS>
-__global__ __launch_bounds__(mmvq_threads<M>())
+__global__ __launch_bounds__((mmvq_threads<M, RS, G>()))
 void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrows, int units_per_row,
                  const block_q8_1 *__restrict__ y1, const block_q8_1 *__restrict__ y2, int y_row_blocks,
                  const float *__restrict__ inverse, void *__restrict__ dst, int64_t stride_dst, int dst_bf16) {
     using U = Unit<TYPE>;
-    constexpr int THREADS = mmvq_threads<M>();
+    constexpr int THREADS = mmvq_threads<M, RS, G>();
     constexpr int BYTES = block_bytes(TYPE);
     constexpr int PASSES = TWO_PASS ? 2 : 1;
     constexpr int ROWS = M * PASSES;  // activation rows staged
@@ -220,7 +227,7 @@ inline int gemv_row_sets(int64_t n, int g) {
 template <int TYPE, int M, bool TWO_PASS, int G, int RS>
 static void launch_sets(const uint8_t *w, int64_t n, int64_t k, const block_q8_1 *y1, const block_q8_1 *y2,
                         const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
-    constexpr int THREADS = mmvq_threads<M>();
+    constexpr int THREADS = mmvq_threads<M, RS, G>();
     // ring depth 2: two units per lane in flight; a deeper ring costs more waves than it
     // hides (measured on MI355X for every shape here, e.g. Q4_K gate/up b2 -14 %, qkv and
     // o_proj -3..-8 % against 3)
