@@ -95,20 +95,29 @@ __device__ __forceinline__ float quad_sum(float v) {
 // Scale of a row from its maximum |x|, read by every workgroup of the row.
 // The row is read in runs of 8 values, run p by thread p % PREP_THREADS; the run this
 // workgroup's thread quantises (blockIdx.y * PREP_THREADS + threadIdx.x: 4 lanes per
-// block, PREP_BLOCKS blocks per workgroup) is kept in `own`, so the values are read once.
+// block, PREP_BLOCKS blocks per workgroup) is kept in `own`, so the values are read once
+// (when that run is past the row end the thread stores nothing).
 template <int DTYPE>
 __device__ __forceinline__ float row_scale(const typename Src<DTYPE>::T *xr, int k, float *lds, float *inverse_out,
                                            bool writer, float (&own)[8]) {
     float mx = 0.0f;
-    int i = 0;
-    for (int p = threadIdx.x; p < k / 8; p += PREP_THREADS, ++i) {
-        float v[8];
-        load8<DTYPE>(xr + 8 * p, v);
+    const int runs = k / 8;
+    // Four runs per round, loaded unconditionally (indices clamped to the last run, whose
+    // values are then ignored) so that they are all in flight before the first maximum.
+    for (int i0 = 0; i0 * PREP_THREADS < runs; i0 += 4) {
+        float v[4][8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[j]));
-        if (i == int(blockIdx.y)) {  // uniform
+        for (int u = 0; u < 4; ++u) load8<DTYPE>(xr + 8 * min(int(threadIdx.x) + (i0 + u) * PREP_THREADS, runs - 1), v[u]);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) own[j] = v[j];
+        for (int u = 0; u < 4; ++u) {
+            if (int(threadIdx.x) + (i0 + u) * PREP_THREADS < runs) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[u][j]));
+            }
+            if (i0 + u == int(blockIdx.y)) {  // uniform
+#pragma unroll
+                for (int j = 0; j < 8; ++j) own[j] = v[u][j];
+            }
         }
     }
     return row_scale_from_max(block_max(mx, lds), inverse_out, writer);
