@@ -23,7 +23,15 @@
 //     products per K step: they run on v_mfma_f32_16x16x4_f32 into the same
 //     accumulators instead of the VALU;
 //   * several waves of a workgroup may split K (KS) when there are too few weight rows
-//     to fill the chip; their partial sums are added in LDS in a fixed order.
+//     to fill the chip; their partial sums are added in LDS in a fixed order;
+//   * up to 8 activation rows (PAIR): two 32-value blocks share one
+//     v_mfma_i32_16x16x64_i8. The B operand is the lane's codes of blocks 2c and 2c+1,
+//     the A operand holds block 2c's activation codes in rows 0-7 and block 2c+1's in
+//     rows 8-15, each zero against the other block's codes, so D rows 0-7 are the dots
+//     of block 2c and rows 8-15 those of block 2c+1 for the same 8 activation rows.
+//     Every element of the fp32 epilogue is then a real one (a 16-row tile would pad 8
+//     rows), which halves the epilogue's VALU work; the two halves are added once at
+//     the end.
 // Operand layouts (checked on gfx950): 16x16x32_i8: lane l holds A row l%16 and B
 // column l%16 for k = 8*(l/16) .. +8; 16x16x4_f32: A row l%16, B column l%16, k = l/16;
 // both: D column l%16, rows 4*(l/16) + i.
@@ -62,12 +70,13 @@ constexpr size_t mmq_lds_bytes() {
     return act > red ? act : red;
 }
 
-template <int TYPE, int TM, int TN, int KS, int DEPTH>
+template <int TYPE, int TM, int TN, int KS, int DEPTH, bool PAIR>
 __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
     const uint8_t *__restrict__ weight, int64_t row_bytes, int n, int k, const block_q8_1 *__restrict__ y,
     int m, const float *__restrict__ inverse, void *__restrict__ dst, int64_t stride_dst, int dst_bf16) {
     using W = MmqLoad<TYPE>;
-    constexpr int MT = 16 * TM, RG = 4 / KS, NT = W::NTERM;
+    static_assert(!PAIR || TM == 1, "paired blocks use one tile of 8 activation rows");
+    constexpr int MT = PAIR ? 8 : 16 * TM, RG = 4 / KS, NT = W::NTERM;
     constexpr int BUF = mmq_buf_bytes<TYPE, TM>();
     constexpr int D8_OFF = MT * 8 * 32, TA_OFF = D8_OFF + MT * 8 * 4;
     constexpr int PAIRS = KS * MT * 8;  // (k-group, row, block) activation blocks per iteration
@@ -165,8 +174,45 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
         const uint8_t *base = kai_mmq_lds + (buf * KS + kg) * BUF;
         const float *d8s = reinterpret_cast<const float *>(base + D8_OFF);
         const v4i_t zero = {0, 0, 0, 0};
+        if constexpr (PAIR) {
+            // lane's A row: activation row col % 8 of block 2c + col / 8; its D rows
+            // 4*oct .. +4: activation rows 4*(oct % 2) .. +4 of block 2c + oct / 2
+            const int mr = col & 7, hi = col >> 3, ob = oct >> 1;
 #pragma unroll
-        for (int b = 0; b < 8; ++b) {
+            for (int c = 0; c < 4; ++c) {
+                const uint64_t aq =
+                    *reinterpret_cast<const uint64_t *>(base + ((2 * c + hi) * MT + mr) * 32 + 8 * (aoct ^ ((mr >> 2) & 3)));
+                const int a0 = static_cast<int>(aq), a1 = static_cast<int>(aq >> 32);
+                const v4i_t av = hi ? v4i_t{0, 0, a0, a1} : v4i_t{a0, a1, 0, 0};
+                const float4 dv = *reinterpret_cast<const float4 *>(d8s + (2 * c + ob) * MT + 4 * (oct & 1));
+                const float d8[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+                for (int t = 0; t < TN; ++t) {
+                    const uint64_t c0 = W::codes(w[t], 2 * c, oct, grid_lds), c1 = W::codes(w[t], 2 * c + 1, oct, grid_lds);
+                    const v4i_t bv = {static_cast<int>(c0), static_cast<int>(c0 >> 32), static_cast<int>(c1),
+                                      static_cast<int>(c1 >> 32)};
+                    const float sa = ob ? W::scale(w[t], 2 * c + 1) : W::scale(w[t], 2 * c);
+                    if constexpr (W::SPLIT16) {
+                        const bool first = W::first_half(oct);
+                        const v4i_t r1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, first ? bv : zero, zero, 0, 0, 0);
+                        const v4i_t r2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, first ? zero : bv, zero, 0, 0, 0);
+                        const int sl = ob ? W::iscale(w[t], 4 * c + 2) : W::iscale(w[t], 4 * c);
+                        const int sh = ob ? W::iscale(w[t], 4 * c + 3) : W::iscale(w[t], 4 * c + 1);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int x = __mul24(sl, r1[i]) + __mul24(sh, r2[i]);
+                            acc[0][t][i] = fmaf(d8[i] * sa, static_cast<float>(x), acc[0][t][i]);
+                        }
+                    } else {
+                        const v4i_t r = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, zero, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[0][t][i] = fmaf(d8[i] * sa, static_cast<float>(r[i]), acc[0][t][i]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < (PAIR ? 0 : 8); ++b) {
             uint64_t bq[TN], bq2[TN];
             float sa[TN];
             int sl[TN], sh[TN];
@@ -215,7 +261,9 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
                 for (int t = 0; t < TN; ++t) bt[t] = W::term(w[t], j, oct);
 #pragma unroll
                 for (int a = 0; a < TM; ++a) {
-                    const float at = ta[(4 * j + oct) * MT + 16 * a + col];
+                    // paired: the terms go to D rows 0-7 (activation rows 0-7), A rows 8-15 zero
+                    const float at = PAIR ? (col < 8 ? ta[(4 * j + oct) * MT + col] : 0.0f)
+                                          : ta[(4 * j + oct) * MT + 16 * a + col];
 #pragma unroll
                     for (int t = 0; t < TN; ++t) acc[a][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(at, bt[t], acc[a][t], 0, 0, 0);
                 }
@@ -274,6 +322,13 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
         }
     }
     if (kg != 0) return;
+    if constexpr (PAIR) {  // D rows 8-15 (lanes 32-63) hold the odd blocks' sums of rows 0-7
+#pragma unroll
+        for (int t = 0; t < TN; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[0][t][i] += __shfl_xor(acc[0][t][i], 32);
+        if (oct >= 2) return;
+    }
 
     // ---- epilogue: x inverse[m], F32 or BF16, strided store
 #pragma unroll
@@ -296,16 +351,16 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
     }
 }
 
-template <int TYPE, int TM, int TN, int KS>
+template <int TYPE, int TM, int TN, int KS, bool PAIR = false>
 static void launch_mmq_tile(const void *weight, int64_t n, int64_t k, const block_q8_1 *y, int64_t m,
                             const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
-    constexpr int MT = 16 * TM, ROWS = 16 * TN * (4 / KS);
+    constexpr int MT = PAIR ? 8 : 16 * TM, ROWS = 16 * TN * (4 / KS);
     const int64_t row_bytes = (k / block_elems(TYPE)) * block_bytes(TYPE);
     const size_t lds = mmq_lds_bytes<TYPE, TM, TN, KS>();
     // weight steps in flight: two (a deeper ring costs resident waves; measured on MI355X
     // at 8-16 rows: Q4_K gate/up -4 %, Q6_K down -3..-5 % against four)
     constexpr int DEPTH = 2;
-    auto kernel = mmq_kernel<TYPE, TM, TN, KS, DEPTH>;
+    auto kernel = mmq_kernel<TYPE, TM, TN, KS, DEPTH, PAIR>;
     static bool attribute_set = false;
     if (!attribute_set) {
         if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -348,6 +403,18 @@ void launch_mmq_type(const void *weight, int64_t n, int64_t k, int64_t m, const 
         }
     }
     const int key = tm * 100 + tn * 10 + ks;
+    if (m <= 8) {  // one tile of 8 activation rows, two blocks per MFMA
+        switch (key) {
+#define KAI_P(TN, KS) \
+    case 100 + TN * 10 + KS: \
+        if constexpr (TN == 1 || wide) \
+            launch_mmq_tile<TYPE, 1, TN, KS, true>(weight, n, k, y, m, inverse, dst, dst_bf16, stride_dst, stream); \
+        return;
+            KAI_P(2, 1) KAI_P(1, 1) KAI_P(2, 2) KAI_P(1, 2) KAI_P(1, 4)
+#undef KAI_P
+            default: throw Error("MMQ tile selection failed");
+        }
+    }
     switch (key) {
 #define KAI_C(TM, TN, KS) \
     case TM * 100 + TN * 10 + KS: \

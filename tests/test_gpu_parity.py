@@ -238,6 +238,29 @@ def test_mmq_each_type(kai, qtype, m, k, n):
     assert O.normwise_rel(out, ref) <= TOL_F32
 
 
+PAIRED = [(O.Q4_K, 5, 768, 200), (O.Q6_K, 8, 1280, 136), (O.Q2_K, 6, 768, 200), (O.Q8_0, 8, 16384, 72),
+          (O.Q4_0, 8, 16384, 40), (O.IQ3_S, 7, 18432, 72)]
+
+
+@pytest.mark.parametrize("qtype,m,k,n", PAIRED, ids=lambda v: str(v))
+@pytest.mark.parametrize("bf16", [False, True])
+def test_mmq_paired_tile(kai, qtype, m, k, n, bf16):
+    """Up to 8 rows on the int8-MFMA GEMM (two 32-value blocks per MFMA), reached through
+    kai_fused_mmvq above the GEMV's row limit or, for the 8-row GEMV formats, above its
+    LDS staging (long K): partial weight tiles, K split over waves, strided bf16 output."""
+    print(f"mmq paired {O.NAMES[qtype]} m={m} k={k} n={n} bf16={bf16}", flush=True)
+    rng = np.random.default_rng(qtype * 100 + m)
+    w = O.random_blocks(qtype, n, k, rng)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    act = gpu_prepare(kai, to_dev(x))
+    out = gpu_mmvq(kai, qtype, to_dev(w), n, k, act, m, bf16=bf16, stride=n + 8 if bf16 else None)
+    ref = O.mul_mat(qtype, w, k, O.prepare(x), m)
+    got = out.float().cpu().numpy()
+    assert O.normwise_rel(got[:, :n], ref) <= (TOL_BF16 if bf16 else TOL_F32)
+    if bf16:
+        assert np.isnan(got[:, n:]).all()
+
+
 @pytest.mark.parametrize("qtype", [O.Q4_K, O.Q6_K, O.IQ3_S])
 def test_mmq_prefill_shape(kai, qtype):
     """A prefill-sized call (m = 512) on a full-width weight, bf16 activations."""
@@ -381,6 +404,7 @@ FULL = [
     ("C2 Q4_0 gate/up", O.Q4_0, 16384, 2048, 8),
     ("C2 Q4_0 down", O.Q4_0, 2048, 8192, 4),
     ("C3 Q4_K gate/up", O.Q4_K, 34816, 5120, 1),
+    ("C3 Q4_K gate/up b8", O.Q4_K, 34816, 5120, 8),
     ("C3 Q4_K qkv", O.Q4_K, 7168, 5120, 16),
     ("C3 Q6_K down", O.Q6_K, 5120, 17408, 2),
     ("C3 Q6_K o_proj", O.Q6_K, 5120, 6144, 8),
