@@ -8,9 +8,9 @@
 //     (gemv_row_sets);
 //     the lanes of a group walk the row's ~32-byte units (kai_units.h) in order, so
 //     each load instruction reads contiguous runs of G units of wire bytes;
-//   * a ring of DEPTH units per lane of wire bytes is kept in flight (1 with one row set,
-//     2 with two): unit t + DEPTH is requested before unit t is multiplied (a shallow ring
-//     keeps more waves resident);
+//   * a ring of DEPTH units per lane of wire bytes is kept in flight (1 for superblock
+//     formats with one row set, else 2): unit t + DEPTH is requested before unit t is
+//     multiplied (a shallow ring keeps more waves resident);
 //   * the activation (all m rows of Q8_1 blocks, byte for byte) is staged in LDS once
 //     per workgroup together with the exact code sums of every 16-value half, so the
 //     loop issues no vector-memory load other than the weight stream (vmcnt retires in
@@ -229,12 +229,14 @@ template <int TYPE, int M, bool TWO_PASS, int G, int RS>
 static void launch_sets(const uint8_t *w, int64_t n, int64_t k, const block_q8_1 *y1, const block_q8_1 *y2,
                         const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
     constexpr int THREADS = mmvq_threads<M, RS, G>();
-    // ring depth: one unit per lane in flight with one row set per wave, two with two row
-    // sets (whose next set's loads overlap the previous set's reduction). A deeper ring
-    // costs more waves than it hides; measured on MI355X: one against two units, Q6_K down
-    // and o_proj -8..-11 %, Q4_K qkv -5..-10 %, but two row sets (Q4_K gate/up) +3 %; two
-    // against three, gate/up b2 -14 %, qkv and o_proj -3..-8 %.
-    constexpr int DEPTH = RS == 1 ? 1 : 2;
+    // ring depth: one unit per lane in flight for the 256-value superblock formats with one
+    // row set per wave; two with two row sets (whose next set's loads overlap the previous
+    // set's reduction) and for the 32-value formats (one small block per unit). A deeper
+    // ring costs more waves than it hides; measured on MI355X, one against two units: Q6_K
+    // down and o_proj -8..-11 %, Q4_K qkv -5..-10 %, Q2_K gate/up -24 %, IQ3_S down
+    // -6..-11 %, but Q4_K gate/up (two row sets) +3 % and Q4_0 down +15 %; two against
+    // three: gate/up b2 -14 %, qkv and o_proj -3..-8 %.
+    constexpr int DEPTH = RS == 1 && block_elems(TYPE) == 256 ? 1 : 2;
     constexpr int QK = block_elems(TYPE);
     const int64_t blocks_per_row = k / QK;
     const int64_t row_bytes = blocks_per_row * block_bytes(TYPE);
