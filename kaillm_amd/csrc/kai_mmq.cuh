@@ -7,7 +7,7 @@
 //
 // Design for gfx950 (wave64, v_mfma_i32_16x16x32_i8):
 //   * each wave owns 16*TN weight rows and streams their wire bytes from HBM straight
-//     into registers (one or two K steps in flight); a lane holds, for its row (lane % 16) and
+//     into registers (one K step in flight); a lane holds, for its row (lane % 16) and
 //     octet (lane / 16), the 8 codes of every 32-value block that the MFMA B operand
 //     needs, so weights never pass through LDS and the wave needs no barrier for them;
 //   * the activation rows of the tile (MT = 16*TM) are staged once per K step into LDS
@@ -357,12 +357,12 @@ static void launch_mmq_tile(const void *weight, int64_t n, int64_t k, const bloc
     constexpr int MT = PAIR ? 8 : 16 * TM, ROWS = 16 * TN * (4 / KS);
     const int64_t row_bytes = (k / block_elems(TYPE)) * block_bytes(TYPE);
     const size_t lds = mmq_lds_bytes<TYPE, TM, TN, KS>();
-    // weight steps in flight: one for the one-tile kernels (up to 16 rows), two for the
-    // larger tiles. The compiler drains every outstanding load before a step's compute (the
-    // loop's branches), so a deeper ring only costs registers and resident waves: Q4_K
-    // gate/up at 8 rows 37.1 / 34.0 / 32.9 us with three / two / one steps on MI355X, and
-    // two against four -4 % at 8-16 rows.
-    constexpr int DEPTH = TM == 1 ? 1 : 2;
+    // weight steps in flight: one. The compiler drains every outstanding load before a
+    // step's compute (the loop's branches), so a deeper ring only costs registers and
+    // resident waves. Measured on MI355X: Q4_K gate/up at 8 rows 37.1 / 34.0 / 32.9 us with
+    // three / two / one steps; at 32-80 rows one against two steps, Q4_0 -5..-13 %, Q6_K
+    // and Q2_K unchanged.
+    constexpr int DEPTH = 1;
     auto kernel = mmq_kernel<TYPE, TM, TN, KS, DEPTH, PAIR>;
     static bool attribute_set = false;
     if (!attribute_set) {
