@@ -5,7 +5,6 @@
 #include <algorithm>
 #include <climits>
 #include <string>
-#include <vector>
 
 #include "../../include/kai_hip.h"
 #include "kai_launch.h"
@@ -47,40 +46,60 @@ struct Group {
     int64_t total_rows = 0;
 };
 
+// The batched entry's shape rule is the reference's validate() (current_ggml_direct.cu:72-97):
+// a supported type, 0 < n, k <= INT_MAX and k a whole number of the type's blocks; m > 8.
 Group validate_group(const int *types, const int64_t *rows, int count, int64_t k, int64_t m) {
     if (!types || !rows || count < 1 || count > MAX_GROUP)
         throw kai::Error("Expected between one and 32 original GGUF matrices");
     if (m <= MAX_FUSED_ROWS || m > INT_MAX) throw kai::Error("Fused MMQ requires more than 8 activation rows");
     Group g;
     for (int i = 0; i < count; ++i) {
-        if (!shape_ok(types[i], rows[i], k, m, INT_MAX)) throw kai::Error("Invalid fused MMQ matrix type or shape");
+        const int qk = kai::block_elems(types[i]);
+        if (!kai::weight_type_supported(types[i]) || rows[i] <= 0 || rows[i] > INT_MAX || k <= 0 || k > INT_MAX ||
+            k % qk)
+            throw kai::Error("Invalid fused MMQ matrix type or shape");
         g.total_rows += rows[i];
     }
     if (g.total_rows % 4 || g.total_rows > INT_MAX) throw kai::Error("Fused MMQ output width must be a multiple of four");
     return g;
 }
 
-// Scratch of one fused MMQ call: the Q8_1 activation buffer, then, when a matrix of the
-// group may run on an fp16-MFMA kernel, their operands, then the small-M GEMM's partial
-// sums (one buffer, reused by the matrices in turn).
+// Scratch of one batched call, each region 256-aligned: [inverse: m fp32] then one plane
+// of GGML MMQ's activation (mmq_plane_bytes) per layout a matrix of the group reads, in the
+// order D4, DS4, D2S6.
 struct MmqScratch {
-    size_t act, mmf, partial;
-    size_t total() const { return act + mmf + partial; }
+    size_t inverse = 0, plane[3] = {0, 0, 0}, total = 0;
+    bool has_plane[3] = {false, false, false};
 };
-MmqScratch mmq_scratch(const int *types, const int64_t *rows, int count, int64_t k, int64_t m) {
-    bool mmf = false, t32 = false, t16 = false;
-    size_t partial = 0;
-    for (int i = 0; i < count; ++i) {
-        if (!kai::fp16_route(types[i], m, rows[i], k)) continue;
-        mmf = true;
-        t32 |= kai::mmf_uses_t32(types[i]);
-        t16 |= kai::mmf_uses_t16(types[i]);
-        if (kai::mfv_route(types[i], m, rows[i], k)) partial = std::max(partial, kai::mfv_partial_bytes(m, rows[i], k));
+MmqScratch mmq_scratch(const int *types, int count, int64_t k, int64_t m) {
+    MmqScratch p;
+    for (int i = 0; i < count; ++i) p.has_plane[kai::mmq_layout(types[i])] = true;
+    size_t off = kai::align256(size_t(m) * sizeof(float));
+    for (int l = 0; l < 3; ++l) {
+        p.plane[l] = off;
+        if (p.has_plane[l]) off += kai::align256(kai::mmq_plane_bytes(m, k));
     }
-    return {kai::activation_bytes(m, k, 0), mmf ? kai::mmf_bytes(m, k, t32, t16) : 0, partial};
+    p.total = off;
+    return p;
 }
-size_t mmq_scratch_bytes(const int *types, const int64_t *rows, int count, int64_t k, int64_t m) {
-    return mmq_scratch(types, rows, count, k, m).total();
+
+// One batched call on a prepared scratch: one preparation writes every plane the group
+// reads, then one int8 GEMM per matrix stores its column slice.
+void run_mmq_group(const void *const *weights, const int *types, const int64_t *rows, int count, const void *x,
+                   int x_dtype, int64_t stride_x, int64_t k, int64_t m, void *dst, bool dst_bf16, int64_t ld,
+                   char *scratch, const MmqScratch &plan, hipStream_t s) {
+    const size_t elem = dst_bf16 ? 2 : 4;
+    float *inverse = reinterpret_cast<float *>(scratch + plan.inverse);
+    uint8_t *planes[3];
+    for (int l = 0; l < 3; ++l)
+        planes[l] = plan.has_plane[l] ? reinterpret_cast<uint8_t *>(scratch + plan.plane[l]) : nullptr;
+    kai::launch_prepare_mmq(x, x_dtype, m, k, stride_x, kai::MmqPlanes{planes[0], planes[1], planes[2], inverse}, s);
+    int64_t col = 0;
+    for (int i = 0; i < count; ++i) {
+        kai::launch_mmq_planes(types[i], weights[i], rows[i], k, m, planes[kai::mmq_layout(types[i])], inverse,
+                               static_cast<char *>(dst) + col * elem, dst_bf16, ld, s);
+        col += rows[i];
+    }
 }
 
 }  // namespace
@@ -204,12 +223,12 @@ extern "C" int kai_fused_mmvq(const void *weight, int type, int64_t n, int64_t k
 
 extern "C" size_t kai_fused_mmq_workspace(int device, const int *types, const int64_t *rows, int count, int64_t k,
                                           int64_t m, int direct_f32) {
-    (void)direct_f32;
+    (void)direct_f32;  // outputs are stored in place with their stride: no staging tile
     try {
         last_error.clear();
         if (device < 0) throw kai::Error("Invalid device index");
         validate_group(types, rows, count, k, m);
-        return mmq_scratch_bytes(types, rows, count, k, m);
+        return mmq_scratch(types, count, k, m).total;
     } catch (const std::exception &error) {
         last_error = error.what();
         return 0;
@@ -222,8 +241,8 @@ extern "C" int kai_fused_mmq_run(const void *const *weights, const int *types, c
                                  uintptr_t stream) {
     return entry([&] {
         const Group g = validate_group(types, rows, count, k, m);
-        const size_t need = mmq_scratch_bytes(types, rows, count, k, m);
-        if (!weights || !x || !dst || !scratch || scratch_bytes < need || k % 4 || stride_x < k || device < 0)
+        const MmqScratch plan = mmq_scratch(types, count, k, m);
+        if (!weights || !x || !dst || !scratch || scratch_bytes < plan.total || k % 4 || stride_x < k || device < 0)
             throw kai::Error("Invalid fused MMQ pointers, strides or scratch capacity");
         for (int i = 0; i < count; ++i)
             if (!weights[i]) throw kai::Error("Null packed matrix");
@@ -232,54 +251,8 @@ extern "C" int kai_fused_mmq_run(const void *const *weights, const int *types, c
         int current = -1;
         if (hipGetDevice(&current) != hipSuccess) throw kai::Error("No HIP device");
         if (current != device && hipSetDevice(device) != hipSuccess) throw kai::Error("Invalid device index");
-        const hipStream_t s = stream_of(stream);
-        const kai::ActLayout l = activation_layout(scratch, m, k, 0);
-        const size_t elem = dst_bf16 ? 2 : 4;
-        // Matrices on the fp16-MFMA kernels (the prefill GEMM for large m with 4-element
-        // aligned output columns, the small-M GEMM up to 16 rows) share one operand
-        // preparation; the others one Q8_1 preparation.
-        enum : char { Q8 = 0, MMF = 1, MFV = 2 };
-        bool any_q8 = false, t32 = false, t16 = false;
-        std::vector<char> path(count);
-        {
-            int64_t c = 0;
-            for (int i = 0; i < count; ++i) {
-                const uintptr_t addr = reinterpret_cast<uintptr_t>(dst) + uintptr_t(c * elem);
-                if (kai::mmf_route(types[i], m, rows[i], k) && ld % 4 == 0 && addr % (4 * elem) == 0) path[i] = MMF;
-                else if (kai::mfv_route(types[i], m, rows[i], k)) path[i] = MFV;
-                else path[i] = Q8;
-                any_q8 |= path[i] == Q8;
-                t32 |= path[i] != Q8 && kai::mmf_uses_t32(types[i]);
-                t16 |= path[i] != Q8 && kai::mmf_uses_t16(types[i]);
-                c += rows[i];
-            }
-        }
-        const MmqScratch plan = mmq_scratch(types, rows, count, k, m);
-        const kai::MmfAct fa = kai::mmf_layout(static_cast<char *>(scratch) + plan.act, m, k, t32, t16);
-        float *partial = reinterpret_cast<float *>(static_cast<char *>(scratch) + plan.act + plan.mmf);
-        if (any_q8) kai::launch_prepare(x, x_dtype, m, k, stride_x, l, s);
-        bool prepared_mmf = false;
-        const int64_t yrb = k / kai::QK8_1;
-        int64_t col = 0;
-        for (int i = 0; i < count; ++i) {
-            char *out = static_cast<char *>(dst) + col * elem;
-            if (path[i] != Q8) {
-                if (!prepared_mmf) kai::launch_prepare_mmf(x, x_dtype, m, k, stride_x, fa, s);
-                prepared_mmf = true;
-                if (path[i] == MMF) kai::launch_mmf(types[i], weights[i], rows[i], k, m, fa, out, dst_bf16 != 0, ld, s);
-                else kai::launch_mfv(types[i], weights[i], rows[i], k, m, fa, partial, out, dst_bf16 != 0, ld, s);
-            } else if (k % 256 == 0) {
-                kai::launch_mmq(types[i], weights[i], rows[i], k, m, l.y1, l.inverse, out, dst_bf16 != 0, ld, s);
-            } else {
-                // k not a multiple of the 256-value MMQ step: GEMV launches of up to 16 rows
-                for (int64_t j0 = 0; j0 < m; j0 += kai::MMVQ_MAX_ROWS) {
-                    const int64_t mm = std::min<int64_t>(kai::MMVQ_MAX_ROWS, m - j0);
-                    kai::launch_mmvq(types[i], weights[i], rows[i], k, mm, l.y1 + j0 * yrb, nullptr, l.inverse + j0,
-                                     out + j0 * ld * elem, dst_bf16 != 0, ld, s);
-                }
-            }
-            col += rows[i];
-        }
+        run_mmq_group(weights, types, rows, count, x, x_dtype, stride_x, k, m, dst, dst_bf16 != 0, ld,
+                      static_cast<char *>(scratch), plan, stream_of(stream));
         if (current != device) (void)hipSetDevice(current);
     });
 }

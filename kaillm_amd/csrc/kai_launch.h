@@ -5,6 +5,8 @@
 
 #include <hip/hip_runtime.h>
 #include <algorithm>
+#include <atomic>
+#include <climits>
 #include <stdexcept>
 #include <string>
 
@@ -21,6 +23,22 @@ constexpr int MMVQ_MAX_ROWS = 16;  // activation rows the GEMV kernel is built f
 
 // Compute units of the current device (cached per device).
 int device_cu_count();
+
+// Devices (bit per index below 64) on which a kernel's dynamic LDS limit is raised.
+using DeviceFlags = std::atomic<uint64_t>;
+// Raise `kernel`'s dynamic LDS limit to `bytes` on the current device the first time it
+// launches there. Callable from any host thread: the flags are atomic and the attribute
+// call is idempotent, so threads racing on a device's first launch both set it; devices
+// from index 64 on set it every launch.
+inline void raise_dynamic_lds(const void *kernel, size_t bytes, DeviceFlags &done, const char *what) {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) throw Error("No HIP device");
+    const uint64_t bit = device < 64 ? uint64_t(1) << device : 0;
+    if (bit && (done.load(std::memory_order_acquire) & bit)) return;
+    if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)) != hipSuccess)
+        throw Error(what);
+    done.fetch_or(bit, std::memory_order_release);
+}
 
 // Activation buffer layout (the reference's, byte for byte): [pass1: m*(k/32) Q8_1 blocks,
 // 256-aligned][pass2 when two_pass][inverse: m floats, 256-aligned].
@@ -90,97 +108,30 @@ inline bool gemv_one_launch(int64_t m, int64_t k, int two_pass) {
 }
 void launch_mmq(int type, const void *weight, int64_t n, int64_t k, int64_t m, const block_q8_1 *y,
                 const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream);
+// The same GEMM over the batched path's activation plane of the type's layout (m > 8;
+// any k that is a whole number of the type's blocks: a short last K step is masked).
+void launch_mmq_planes(int type, const void *weight, int64_t n, int64_t k, int64_t m, const uint8_t *plane,
+                       const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream);
 
-// Prefill GEMM on fp16 MFMA (kai_mmf.cuh) for K-quant weights from MMF_MIN_ROWS rows on.
-// Its activation operands, one region each, 256-aligned: a16 [m][k] fp16 = half(d8 * q8) of
-// the row's Q8_1 blocks, in the GEMM's K order (mmf_a16_run); t32 [m][k/256][64 bytes] and
-// t16 [m][k/256][96 bytes], the min-term operands of 32- and 16-value sums (present when a
-// matrix of the group needs them); inverse [m] fp32.
-// Tiles of the fp16-MFMA GEMM (kai_mmf.cuh: 256 weight rows x 96 activation rows); below
-// MMF_MIN_TILES workgroups it fills too little of the chip and the int8 kernel is faster
-// (measured crossover on MI355X at 120-170 tiles).
-constexpr int MMF_TILE_N = 256, MMF_TILE_M = 96, MMF_MIN_TILES = 160;
-constexpr int MMF_MIN_ROWS = 128;
-// K order of a16 within a superblock, in runs of 8 values: the GEMM's step j (64 values)
-// holds at run 8 j + 4 h + g, for lane group g and half h, block 4 (j / 2) + 2 (g / 2) + h
-// at positions 16 (g % 2) + 8 (j % 2) + [0, 8). Every step then takes, per weight row and
-// lane group, 8 code bytes of one 16-byte run of the Q4_K superblock (a pair of steps
-// shares it), so a lane loads its codes as one 16-byte piece per two steps. Returns the
-// run of block `block` (0..7) positions [8 run, 8 run + 8).
-__host__ __device__ inline int mmf_a16_run(int block, int run) {
-    const int j = 2 * (block >> 2) + (run & 1), g = 2 * ((block >> 1) & 1) + (run >> 1), h = block & 1;
-    return 8 * j + 4 * h + g;
+// Batched path (kai_fused_mmq_run): activation planes of GGML's MMQ quantisation, one per
+// layout a matrix of the group reads (D4: Q8_0, Q6_K, IQ3_S; DS4: Q4_0, Q4_K; D2S6: Q2_K).
+// A plane holds 128-value blocks of MMQ_BLOCK_BYTES (16 header bytes, int8 qs[128]) in
+// [K/128][m] order, K padded to a multiple of MMQ_ROW_PADDING with zero blocks (the
+// reference's block_q8_1_mmq layout and padding, current_ggml_direct.cu:1025-1092,1136).
+constexpr int MMQ_BLOCK_BYTES = 144, MMQ_ROW_PADDING = 512;
+enum MmqLayout : int { MMQ_D4 = 0, MMQ_DS4 = 1, MMQ_D2S6 = 2 };
+constexpr int mmq_layout(int type) {
+    return type == Q4_0 || type == Q4_K ? MMQ_DS4 : type == Q2_K ? MMQ_D2S6 : MMQ_D4;
 }
-struct MmfAct {
-    uint16_t *a16;
-    uint8_t *t32;
-    uint8_t *t16;
+inline int64_t mmq_blocks128(int64_t k) { return (k + MMQ_ROW_PADDING - 1) / MMQ_ROW_PADDING * (MMQ_ROW_PADDING / 128); }
+inline size_t mmq_plane_bytes(int64_t m, int64_t k) {
+    return size_t(mmq_blocks128(k)) * size_t(m) * MMQ_BLOCK_BYTES;
+}
+struct MmqPlanes {
+    uint8_t *d4, *ds4, *d2s6;  // null when no matrix of the group reads that layout
     float *inverse;
 };
-bool mmf_supported(int type);
-inline bool mmf_uses_t32(int type) { return type == Q4_K; }
-inline bool mmf_uses_t16(int type) { return type == Q2_K; }
-// Whether an m-row product with this matrix runs on the fp16-MFMA GEMM (its weight is
-// addressed through one buffer descriptor: below 4 GiB).
-inline bool mmf_weight_fits(int type, int64_t n, int64_t k) {
-    return n * (k / 256) * block_bytes(type) <= int64_t(UINT32_MAX);
-}
-inline bool mmf_route(int type, int64_t m, int64_t n, int64_t k) {
-    const int64_t tiles = ((m + MMF_TILE_M - 1) / MMF_TILE_M) * ((n + MMF_TILE_N - 1) / MMF_TILE_N);
-    return mmf_supported(type) && m >= MMF_MIN_ROWS && tiles >= MMF_MIN_TILES && k % 256 == 0 &&
-           m * k * 2 <= INT32_MAX && n % 4 == 0 && mmf_weight_fits(type, n, k);
-}
-inline size_t mmf_bytes(int64_t m, int64_t k, bool t32, bool t16) {
-    return align256(size_t(m) * size_t(k) * 2) + (t32 ? align256(size_t(m) * size_t(k / 256) * 64) : 0) +
-           (t16 ? align256(size_t(m) * size_t(k / 256) * 96) : 0) + align256(size_t(m) * sizeof(float));
-}
-inline MmfAct mmf_layout(void *base, int64_t m, int64_t k, bool t32, bool t16) {
-    char *p = static_cast<char *>(base);
-    MmfAct a{};
-    a.a16 = reinterpret_cast<uint16_t *>(p);
-    p += align256(size_t(m) * size_t(k) * 2);
-    if (t32) {
-        a.t32 = reinterpret_cast<uint8_t *>(p);
-        p += align256(size_t(m) * size_t(k / 256) * 64);
-    }
-    if (t16) {
-        a.t16 = reinterpret_cast<uint8_t *>(p);
-        p += align256(size_t(m) * size_t(k / 256) * 96);
-    }
-    a.inverse = reinterpret_cast<float *>(p);
-    return a;
-}
-void launch_prepare_mmf(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const MmfAct &out,
+void launch_prepare_mmq(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const MmqPlanes &planes,
                         hipStream_t stream);
-
-// Small-M GEMM on fp16 MFMA (kai_mfv.cuh), up to MFV_MAX_ROWS activation rows, on the
-// operands of launch_prepare_mmf. Workgroups of 64 weight rows; K is split over
-// mfv_splits(n, k) workgroups (doubling while there are fewer than two workgroups per CU of
-// a 256-CU device and every split keeps at least 4 superblocks), whose fp32 partial sums
-// ([splits][m][n], mfv_partial_bytes) are added by a second kernel.
-constexpr int MFV_MAX_ROWS = 16;
-inline int mfv_splits(int64_t n, int64_t k) {
-    const int64_t wgs = (n + 63) / 64, nsb = k / 256;
-    int ks = 1;
-    while (ks < 8 && wgs * ks < 512 && nsb / (2 * ks) >= 4) ks *= 2;
-    return ks;
-}
-inline size_t mfv_partial_bytes(int64_t m, int64_t n, int64_t k) {
-    const int ks = mfv_splits(n, k);
-    return ks > 1 ? align256(size_t(ks) * size_t(m) * size_t(n) * sizeof(float)) : 0;
-}
-bool mfv_supported(int type);
-inline bool mfv_route(int type, int64_t m, int64_t n, int64_t k) {
-    return mfv_supported(type) && m >= 1 && m <= MFV_MAX_ROWS && k % 256 == 0 && n <= INT32_MAX &&
-           mmf_weight_fits(type, n, k);
-}
-// Whether an m-row product with this matrix runs on one of the fp16-MFMA kernels.
-inline bool fp16_route(int type, int64_t m, int64_t n, int64_t k) {
-    return mmf_route(type, m, n, k) || mfv_route(type, m, n, k);
-}
-void launch_mfv(int type, const void *weight, int64_t n, int64_t k, int64_t m, const MmfAct &act, float *partial,
-                void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream);
-void launch_mmf(int type, const void *weight, int64_t n, int64_t k, int64_t m, const MmfAct &act, void *dst,
-                bool dst_bf16, int64_t stride_dst, hipStream_t stream);
 
 }  // namespace kai

@@ -1,9 +1,13 @@
 // Batched GEMM for more than 8 activation rows (kernels 2 and 3): multi-sequence
 // decode, spec-verify (m = 16..80) and prefill (m = 512..2048), on int8 MFMA.
 //
-// Y[m, n] = inverse[m] * sum_b dot(W[n, b], q8[m, b]): the same exact per-block integer
-// dot products and fp32 scalings as the GEMV (reference: kai_fused_mmq_run,
-// vllm_gguf_plugin/native/kernels/current_ggml_direct.cu:1196-1265).
+// Y[m, n] = inverse[m] * sum_b dot(W[n, b], q8[m, b]) with exact per-block integer dots
+// and fp32 scalings. Two activations: the decode path's Q8_1 blocks (up to 8 rows, paired
+// tile, reached from kai_fused_mmvq) and the batched path's planes of GGML MMQ
+// quantisation (kai_fused_mmq_run, current_ggml_direct.cu:1025-1092,1196-1265), whose
+// layout per format fixes the activation scale (fp32 per 32 values for D4, fp16 per 32
+// for DS4, fp16 per 64 for D2S6) and the min-term sums (stored fp16 sums for DS4, per-16
+// sums of D2S6 for the first 96 values of each 128, code sums times d elsewhere).
 //
 // Design for gfx950 (wave64, v_mfma_i32_16x16x32_i8):
 //   * each wave owns 16*TN weight rows and streams their wire bytes from HBM straight
@@ -58,6 +62,35 @@ __device__ __forceinline__ void act_terms(const uint4 q0, const uint4 q1, uint32
     }
 }
 
+// Scale d8 and min-term activation factors of 32-value block b (0..7 of the K step) of one
+// row, from the batched path's plane: h0 is the header word of the block (D4: fp32 d;
+// DS4: half2 (d, sum); D2S6: half2 of the two per-64 scales), h1 the D2S6 word of stored
+// per-16 sums of the block (absent for the last 32 values of a 128-value block).
+template <int TYPE>
+__device__ __forceinline__ float plane_terms(const uint4 q0, const uint4 q1, uint32_t h0, uint32_t h1, int b,
+                                             float *t) {
+    constexpr int L = mmq_layout(TYPE);
+    float d8;
+    if constexpr (L == MMQ_D4) d8 = __builtin_bit_cast(float, h0);
+    else if constexpr (L == MMQ_DS4) d8 = half_bits_to_float(h0 & 0xffffu);
+    else d8 = half_bits_to_float((h0 >> (16 * ((b & 3) >> 1))) & 0xffffu);
+    const uint4 ones = make_uint4(0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u);
+    if constexpr (TYPE == Q4_0) {
+        t[0] = d8 * static_cast<float>(dot16(ones, q0) + dot16(ones, q1));
+    } else if constexpr (TYPE == Q4_K) {
+        t[0] = half_bits_to_float(h0 >> 16);
+    } else if constexpr (TYPE == Q2_K) {
+        if ((b & 3) < 3) {
+            t[0] = half_bits_to_float(h1 & 0xffffu);
+            t[1] = half_bits_to_float(h1 >> 16);
+        } else {
+            t[0] = d8 * static_cast<float>(dot16(ones, q0));
+            t[1] = d8 * static_cast<float>(dot16(ones, q1));
+        }
+    }
+    return d8;
+}
+
 template <int TYPE, int TM>
 constexpr int mmq_buf_bytes() {  // one K step of MT activation rows in LDS
     return 16 * TM * (8 * 32 + 8 * 4 + MmqW<TYPE>::NTERM * 4);
@@ -70,12 +103,16 @@ constexpr size_t mmq_lds_bytes() {
     return act > red ? act : red;
 }
 
+// PAIR: up to 8 rows of decode Q8_1 blocks (act: block_q8_1 [m][k/32], k % 256 == 0);
+// otherwise the batched path's plane of the type's layout (act: uint8 plane), any k that is
+// a whole number of blocks (a short last step reads zero activations).
 template <int TYPE, int TM, int TN, int KS, int DEPTH, bool PAIR>
 __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
-    const uint8_t *__restrict__ weight, int64_t row_bytes, int n, int k, const block_q8_1 *__restrict__ y,
+    const uint8_t *__restrict__ weight, int64_t row_bytes, int n, int k, const void *__restrict__ act,
     int m, const float *__restrict__ inverse, void *__restrict__ dst, int64_t stride_dst, int dst_bf16) {
     using W = MmqLoad<TYPE>;
     static_assert(!PAIR || TM == 1, "paired blocks use one tile of 8 activation rows");
+    constexpr int MODE = W::template mode<!PAIR>();  // decode (paired) or batched arithmetic
     constexpr int MT = PAIR ? 8 : 16 * TM, RG = 4 / KS, NT = W::NTERM;
     constexpr int BUF = mmq_buf_bytes<TYPE, TM>();
     constexpr int D8_OFF = MT * 8 * 32, TA_OFF = D8_OFF + MT * 8 * 4;
@@ -87,7 +124,7 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
     const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
     const int rg = wave % RG, kg = wave / RG;
     const int col = lane % 16, oct = lane / 16;
-    const int nb = k / QK8_1, steps = k / MMQ_STEP;
+    const int nb = k / QK8_1, steps = (k + MMQ_STEP - 1) / MMQ_STEP;
     const int iters = (steps + KS - 1) / KS;
     const int m0 = blockIdx.y * MT;
     const int nrow0 = blockIdx.x * (16 * TN * RG) + rg * 16 * TN;
@@ -100,7 +137,7 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
 
     // ---- activation staging: global Q8_1 blocks -> registers -> LDS (MFMA layout)
     uint4 aq0[PP], aq1[PP];
-    uint32_t ads[PP];
+    uint32_t ads[PP], ads2[PP];
     auto aload = [&](int it) {
 #pragma unroll
         for (int p = 0; p < PP; ++p) {
@@ -108,12 +145,29 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
             const int r = idx % MT, b = (idx / MT) % 8, g = idx / (MT * 8);
             const int s = it * KS + g, row = m0 + r;
             aq0[p] = aq1[p] = make_uint4(0, 0, 0, 0);
-            ads[p] = 0;
+            ads[p] = ads2[p] = 0;
             if (idx < PAIRS && s < steps && row < m) {
-                const uint8_t *src = reinterpret_cast<const uint8_t *>(y + int64_t(row) * nb + 8 * s + b);
-                ads[p] = load_unaligned<uint32_t>(src);
-                aq0[p] = load_unaligned<uint4>(src + 4);
-                aq1[p] = load_unaligned<uint4>(src + 20);
+                if constexpr (PAIR) {
+                    const uint8_t *src = reinterpret_cast<const uint8_t *>(
+                        static_cast<const block_q8_1 *>(act) + int64_t(row) * nb + 8 * s + b);
+                    ads[p] = load_unaligned<uint32_t>(src);
+                    aq0[p] = load_unaligned<uint4>(src + 4);
+                    aq1[p] = load_unaligned<uint4>(src + 20);
+                } else {
+                    // 128-value block 2s + b/4 of the row; 32-value block b % 4 inside it
+                    const int sub = b & 3;
+                    const uint8_t *blk = static_cast<const uint8_t *>(act) +
+                                         (int64_t(2 * s + (b >> 2)) * m + row) * MMQ_BLOCK_BYTES;
+                    const uint32_t *hdr = reinterpret_cast<const uint32_t *>(blk);
+                    if constexpr (mmq_layout(TYPE) == MMQ_D2S6) {
+                        ads[p] = hdr[0];
+                        ads2[p] = sub < 3 ? hdr[1 + sub] : 0u;
+                    } else {
+                        ads[p] = hdr[sub];
+                    }
+                    aq0[p] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * sub);
+                    aq1[p] = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * sub);
+                }
             }
         }
     };
@@ -133,11 +187,15 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
                 const uint4 h1 = sw & 1 ? make_uint4(aq1[p].z, aq1[p].w, aq1[p].x, aq1[p].y) : aq1[p];
                 q[sw >> 1] = h0;
                 q[(sw >> 1) ^ 1] = h1;
-                const float d8 = half_bits_to_float(ads[p] & 0xffffu);
+                float d8, t[2];
+                if constexpr (PAIR) {
+                    d8 = half_bits_to_float(ads[p] & 0xffffu);
+                    act_terms<TYPE>(aq0[p], aq1[p], ads[p], d8, t);
+                } else {
+                    d8 = plane_terms<TYPE>(aq0[p], aq1[p], ads[p], ads2[p], b, t);
+                }
                 reinterpret_cast<float *>(base + D8_OFF)[b * MT + r] = d8;
                 if constexpr (NT > 0) {
-                    float t[2];
-                    act_terms<TYPE>(aq0[p], aq1[p], ads[p], d8, t);
                     float *ta = reinterpret_cast<float *>(base + TA_OFF);
                     if constexpr (NT == 8) {
                         ta[b * MT + r] = t[0];
@@ -155,8 +213,9 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
     auto wload = [&](typename W::Raw (&w)[TN], int it) {
         const int s = it * KS + kg;
         if (s < steps) {
+            const int nvalid = min(8, nb - 8 * s);  // 32-value blocks of this step inside the row
 #pragma unroll
-            for (int t = 0; t < TN; ++t) W::load(w[t], wrow[t] + int64_t(s) * W::SB, oct);
+            for (int t = 0; t < TN; ++t) W::load(w[t], wrow[t] + int64_t(s) * W::SB, oct, nvalid);
         }
     };
 
@@ -188,11 +247,12 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
                 const float d8[4] = {dv.x, dv.y, dv.z, dv.w};
 #pragma unroll
                 for (int t = 0; t < TN; ++t) {
-                    const uint64_t c0 = W::codes(w[t], 2 * c, oct, grid_lds), c1 = W::codes(w[t], 2 * c + 1, oct, grid_lds);
+                    const uint64_t c0 = W::template codes<false>(w[t], 2 * c, oct, grid_lds),
+                                   c1 = W::template codes<false>(w[t], 2 * c + 1, oct, grid_lds);
                     const v4i_t bv = {static_cast<int>(c0), static_cast<int>(c0 >> 32), static_cast<int>(c1),
                                       static_cast<int>(c1 >> 32)};
-                    const float sa = ob ? W::scale(w[t], 2 * c + 1) : W::scale(w[t], 2 * c);
-                    if constexpr (W::SPLIT16) {
+                    const float sa = ob ? W::template scale<false>(w[t], 2 * c + 1) : W::template scale<false>(w[t], 2 * c);
+                    if constexpr (MODE == MMQ_ISPLIT) {
                         const bool first = W::first_half(oct);
                         const v4i_t r1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, first ? bv : zero, zero, 0, 0, 0);
                         const v4i_t r2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, first ? zero : bv, zero, 0, 0, 0);
@@ -214,21 +274,28 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
 #pragma unroll
         for (int b = 0; b < (PAIR ? 0 : 8); ++b) {
             uint64_t bq[TN], bq2[TN];
-            float sa[TN];
+            float sa[TN], fl[TN], fh[TN];
             int sl[TN], sh[TN];
 #pragma unroll
             for (int t = 0; t < TN; ++t) {
-                const uint64_t c = W::codes(w[t], b, oct, grid_lds);
-                if constexpr (W::SPLIT16) {
+                const uint64_t c = W::template codes<true>(w[t], b, oct, grid_lds);
+                if constexpr (MODE != MMQ_BLOCK) {
                     const bool first = W::first_half(oct);
                     bq[t] = first ? c : 0ull;
                     bq2[t] = first ? 0ull : c;
-                    sl[t] = W::iscale(w[t], 2 * b);
-                    sh[t] = W::iscale(w[t], 2 * b + 1);
                 } else {
                     bq[t] = c;
                 }
-                sa[t] = W::scale(w[t], b);
+                if constexpr (MODE == MMQ_ISPLIT) {
+                    sl[t] = W::iscale(w[t], 2 * b);
+                    sh[t] = W::iscale(w[t], 2 * b + 1);
+                }
+                if constexpr (MODE == MMQ_FSPLIT) {
+                    fl[t] = W::fscale(w[t], 2 * b);
+                    fh[t] = W::fscale(w[t], 2 * b + 1);
+                } else {
+                    sa[t] = W::template scale<true>(w[t], b);
+                }
             }
 #pragma unroll
             for (int a = 0; a < TM; ++a) {
@@ -238,12 +305,19 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
 #pragma unroll
                 for (int t = 0; t < TN; ++t) {
                     const v4i_t c = __builtin_amdgcn_mfma_i32_16x16x32_i8(aq, static_cast<long>(bq[t]), zero, 0, 0, 0);
-                    if constexpr (W::SPLIT16) {
+                    if constexpr (MODE == MMQ_ISPLIT) {
                         const v4i_t c2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(aq, static_cast<long>(bq2[t]), zero, 0, 0, 0);
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             const int x = __mul24(sl[t], c[i]) + __mul24(sh[t], c2[i]);
                             acc[a][t][i] = fmaf(d8[i] * sa[t], static_cast<float>(x), acc[a][t][i]);
+                        }
+                    } else if constexpr (MODE == MMQ_FSPLIT) {
+                        const v4i_t c2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(aq, static_cast<long>(bq2[t]), zero, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const float x = fmaf(fh[t], static_cast<float>(c2[i]), fl[t] * static_cast<float>(c[i]));
+                            acc[a][t][i] = fmaf(d8[i], x, acc[a][t][i]);
                         }
                     } else {
 #pragma unroll
@@ -258,7 +332,7 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
             for (int j = 0; j < NT / 4; ++j) {
                 float bt[TN];
 #pragma unroll
-                for (int t = 0; t < TN; ++t) bt[t] = W::term(w[t], j, oct);
+                for (int t = 0; t < TN; ++t) bt[t] = W::template term<!PAIR>(w[t], j, oct);
 #pragma unroll
                 for (int a = 0; a < TM; ++a) {
                     // paired: the terms go to D rows 0-7 (activation rows 0-7), A rows 8-15 zero
@@ -352,7 +426,7 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
 }
 
 template <int TYPE, int TM, int TN, int KS, bool PAIR = false>
-static void launch_mmq_tile(const void *weight, int64_t n, int64_t k, const block_q8_1 *y, int64_t m,
+static void launch_mmq_tile(const void *weight, int64_t n, int64_t k, const void *act, int64_t m,
                             const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
     constexpr int MT = PAIR ? 8 : 16 * TM, ROWS = 16 * TN * (4 / KS);
     const int64_t row_bytes = (k / block_elems(TYPE)) * block_bytes(TYPE);
@@ -364,16 +438,11 @@ static void launch_mmq_tile(const void *weight, int64_t n, int64_t k, const bloc
     // and Q2_K unchanged.
     constexpr int DEPTH = 1;
     auto kernel = mmq_kernel<TYPE, TM, TN, KS, DEPTH, PAIR>;
-    static bool attribute_set = false;
-    if (!attribute_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                static_cast<int>(lds)) != hipSuccess)
-            throw Error("Cannot raise the MMQ dynamic LDS limit");
-        attribute_set = true;
-    }
+    static DeviceFlags lds_raised;
+    raise_dynamic_lds(reinterpret_cast<const void *>(kernel), lds, lds_raised, "Cannot raise the MMQ dynamic LDS limit");
     const dim3 grid(static_cast<unsigned>((n + ROWS - 1) / ROWS), static_cast<unsigned>((m + MT - 1) / MT));
     kernel<<<grid, MMQ_THREADS, lds, stream>>>(static_cast<const uint8_t *>(weight), row_bytes, static_cast<int>(n),
-                                               static_cast<int>(k), y, static_cast<int>(m), inverse, dst, stride_dst,
+                                               static_cast<int>(k), act, static_cast<int>(m), inverse, dst, stride_dst,
                                                dst_bf16 ? 1 : 0);
 }
 
@@ -385,10 +454,15 @@ static void launch_mmq_tile(const void *weight, int64_t n, int64_t k, const bloc
 // stays within 80 KiB so that two fit on a CU.
 constexpr bool mmq_allowed(int tm, int ks) { return ks == 1 || (ks == 2 && tm <= 3) || (ks == 4 && tm == 1); }
 
-template <int TYPE>
-void launch_mmq_type(const void *weight, int64_t n, int64_t k, int64_t m, const block_q8_1 *y, const float *inverse,
+// PLANES: act is the batched path's plane of the type's layout (kai_fused_mmq_run, any m,
+// k a whole number of blocks); otherwise decode Q8_1 blocks, up to 8 rows on the paired
+// tile (kai_fused_mmvq), k % 256 == 0.
+template <int TYPE, bool PLANES>
+void launch_mmq_type(const void *weight, int64_t n, int64_t k, int64_t m, const void *act, const float *inverse,
                      void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
-    if (k % MMQ_STEP) throw Error("MMQ needs k to be a multiple of 256");
+    if (!PLANES && k % MMQ_STEP) throw Error("MMQ on decode activations needs k to be a multiple of 256");
+    if (!PLANES && m > 8) throw Error("MMQ on decode activations takes at most 8 rows");
+    if (k % block_elems(TYPE)) throw Error("MMQ needs k to be a whole number of weight blocks");
     static constexpr int CFG[5][2] = {{2, 1}, {1, 1}, {2, 2}, {1, 2}, {1, 4}};
     // Q4_0 keeps 24 registers of wire bytes per row tile and K step: one tile per wave
     constexpr bool wide = TYPE != Q4_0;
@@ -406,30 +480,31 @@ void launch_mmq_type(const void *weight, int64_t n, int64_t k, int64_t m, const 
         }
     }
     const int key = tm * 100 + tn * 10 + ks;
-    if (m <= 8) {  // one tile of 8 activation rows, two blocks per MFMA
+    if constexpr (!PLANES) {  // one tile of 8 activation rows, two blocks per MFMA
         switch (key) {
 #define KAI_P(TN, KS) \
     case 100 + TN * 10 + KS: \
         if constexpr (TN == 1 || wide) \
-            launch_mmq_tile<TYPE, 1, TN, KS, true>(weight, n, k, y, m, inverse, dst, dst_bf16, stride_dst, stream); \
+            launch_mmq_tile<TYPE, 1, TN, KS, true>(weight, n, k, act, m, inverse, dst, dst_bf16, stride_dst, stream); \
         return;
             KAI_P(2, 1) KAI_P(1, 1) KAI_P(2, 2) KAI_P(1, 2) KAI_P(1, 4)
 #undef KAI_P
             default: throw Error("MMQ tile selection failed");
         }
-    }
-    switch (key) {
+    } else {
+        switch (key) {
 #define KAI_C(TM, TN, KS) \
     case TM * 100 + TN * 10 + KS: \
         if constexpr (TN == 1 || wide) \
-            launch_mmq_tile<TYPE, TM, TN, KS>(weight, n, k, y, m, inverse, dst, dst_bf16, stride_dst, stream); \
+            launch_mmq_tile<TYPE, TM, TN, KS>(weight, n, k, act, m, inverse, dst, dst_bf16, stride_dst, stream); \
         break;
-        KAI_C(1, 2, 1) KAI_C(1, 1, 1) KAI_C(1, 2, 2) KAI_C(1, 1, 2) KAI_C(1, 1, 4)
-        KAI_C(2, 2, 1) KAI_C(2, 1, 1) KAI_C(2, 2, 2) KAI_C(2, 1, 2)
-        KAI_C(3, 2, 1) KAI_C(3, 1, 1) KAI_C(3, 2, 2) KAI_C(3, 1, 2)
-        KAI_C(4, 2, 1) KAI_C(4, 1, 1) KAI_C(5, 2, 1) KAI_C(5, 1, 1)
+            KAI_C(1, 2, 1) KAI_C(1, 1, 1) KAI_C(1, 2, 2) KAI_C(1, 1, 2) KAI_C(1, 1, 4)
+            KAI_C(2, 2, 1) KAI_C(2, 1, 1) KAI_C(2, 2, 2) KAI_C(2, 1, 2)
+            KAI_C(3, 2, 1) KAI_C(3, 1, 1) KAI_C(3, 2, 2) KAI_C(3, 1, 2)
+            KAI_C(4, 2, 1) KAI_C(4, 1, 1) KAI_C(5, 2, 1) KAI_C(5, 1, 1)
 #undef KAI_C
-        default: throw Error("MMQ tile selection failed");
+            default: throw Error("MMQ tile selection failed");
+        }
     }
 }
 

@@ -21,6 +21,12 @@ constexpr int MMQ_THREADS = 256;
 constexpr int MMQ_STEP = 256;  // values per K step (one superblock, or 8 blocks of 32)
 
 __device__ __forceinline__ uint64_t u64(uint2 v) { return uint64_t(v.x) | (uint64_t(v.y) << 32); }
+// v rounded to fp16 and back: the half products GGML MMQ's tile loaders form.
+__device__ __forceinline__ float half_round(float v) { return half_bits_to_float(float_to_half_bits(v)); }
+
+// Epilogue of one 32-value block: one MFMA with a block scale (BLOCK), or two MFMAs over
+// its 16-value halves combined with integer scales (ISPLIT) or with fp32 scales (FSPLIT).
+enum MmqMode : int { MMQ_BLOCK = 0, MMQ_ISPLIT = 1, MMQ_FSPLIT = 2 };
 __device__ __forceinline__ uint32_t bits(uint32_t w, uint32_t shift, uint32_t width) {
     return (w >> shift) & ((1u << width) - 1u);
 }
@@ -30,50 +36,58 @@ __device__ __forceinline__ uint32_t bits(uint32_t w, uint32_t shift, uint32_t wi
 // row (load), the int8 codes of its octet of block kb (codes), the scale of block kb
 // (scale: multiplies d8 * C), and the weight factors of the min terms (term: the B
 // operand of the fp32 MFMA for terms 4j .. 4j+3, the lane taking term 4j + oct).
+// The template flag MMA selects the batched path's weight arithmetic (GGML MMQ's tensor-
+// core tile loaders, which round d*sc and dmin*m to fp16 for Q4_K and Q2_K and scale Q2_K
+// per 16 values) over the decode path's (MMVQ, exact products).
 template <int TYPE> struct MmqW;
 
 // Q8_0: 8 blocks of 34 bytes per step. y += d8 * d * C. vecdotq.cuh:165-177.
 template <> struct MmqW<Q8_0> {
     static constexpr int SB = 8 * 34, NTERM = 0;
-    static constexpr bool SPLIT16 = false;
     struct Raw {
         uint2 q[8];
         uint32_t d[8];
     };
-    static __device__ void load(Raw &r, const uint8_t *p, int o) {
+    // nvalid < 8 only on a short last K step: blocks past the row end re-read its last block
+    // (their activation is zero)
+    static __device__ void load(Raw &r, const uint8_t *p, int o, int nvalid) {
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
-            r.d[b] = load_unaligned<uint16_t>(p + 34 * b);
-            r.q[b] = load_unaligned<uint2>(p + 34 * b + 2 + 8 * o);
+            const int c = nvalid == 8 ? b : min(b, nvalid - 1);
+            r.d[b] = load_unaligned<uint16_t>(p + 34 * c);
+            r.q[b] = load_unaligned<uint2>(p + 34 * c + 2 + 8 * o);
         }
     }
-    static __device__ uint64_t codes(const Raw &r, int b, int, const uint32_t *) { return u64(r.q[b]); }
-    static __device__ float scale(const Raw &r, int b) { return half_bits_to_float(r.d[b]); }
-    static __device__ float term(const Raw &, int, int) { return 0.0f; }
+    template <bool MMA> static constexpr int mode() { return MMQ_BLOCK; }
+    template <bool MMA> static __device__ uint64_t codes(const Raw &r, int b, int, const uint32_t *) { return u64(r.q[b]); }
+    template <bool MMA> static __device__ float scale(const Raw &r, int b) { return half_bits_to_float(r.d[b]); }
+    template <bool MMA> static __device__ float term(const Raw &, int, int) { return 0.0f; }
 };
 
 // Q4_0: 8 blocks of 18 bytes; value v < 16 is the low nibble of qs[v], v >= 16 the high
-// nibble of qs[v - 16]. y += d * (d8 * C - 8 * s8), s8 the stored fp16 d8*sum(q8).
-// vecdotq.cuh:46-66.
+// nibble of qs[v - 16]. y += d * (d8 * C - 8 * t): t is the stored fp16 d8*sum(q8) on the
+// decode activation (vecdotq.cuh:46-66), d8 * sum(q8) on the batched one (GGML MMQ's
+// tensor-core tile takes the codes minus 8).
 template <> struct MmqW<Q4_0> {
     static constexpr int SB = 8 * 18, NTERM = 8;
-    static constexpr bool SPLIT16 = false;
     struct Raw {
         uint2 q[8];
         uint32_t d[8];
     };
-    static __device__ void load(Raw &r, const uint8_t *p, int o) {
+    static __device__ void load(Raw &r, const uint8_t *p, int o, int nvalid) {
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
-            r.d[b] = load_unaligned<uint16_t>(p + 18 * b);
-            r.q[b] = load_unaligned<uint2>(p + 18 * b + 2 + 8 * (o & 1));
+            const int c = nvalid == 8 ? b : min(b, nvalid - 1);
+            r.d[b] = load_unaligned<uint16_t>(p + 18 * c);
+            r.q[b] = load_unaligned<uint2>(p + 18 * c + 2 + 8 * (o & 1));
         }
     }
-    static __device__ uint64_t codes(const Raw &r, int b, int o, const uint32_t *) {
+    template <bool MMA> static constexpr int mode() { return MMQ_BLOCK; }
+    template <bool MMA> static __device__ uint64_t codes(const Raw &r, int b, int o, const uint32_t *) {
         return (u64(r.q[b]) >> (4 * (o >> 1))) & 0x0f0f0f0f0f0f0f0full;
     }
-    static __device__ float scale(const Raw &r, int b) { return half_bits_to_float(r.d[b]); }
-    static __device__ float term(const Raw &r, int j, int o) {  // block 4j + o: -8 d
+    template <bool MMA> static __device__ float scale(const Raw &r, int b) { return half_bits_to_float(r.d[b]); }
+    template <bool MMA> static __device__ float term(const Raw &r, int j, int o) {  // block 4j + o: -8 d
         const uint32_t d = o == 0 ? r.d[4 * j] : o == 1 ? r.d[4 * j + 1] : o == 2 ? r.d[4 * j + 2] : r.d[4 * j + 3];
         return -8.0f * half_bits_to_float(d);
     }
@@ -81,35 +95,38 @@ template <> struct MmqW<Q4_0> {
 
 // Q4_K superblock: d, dmin (fp16), 12 bytes of 6-bit scales/mins, qs[128]. Chunk c holds
 // blocks 2c (low nibbles) and 2c+1 (high nibbles); octet o of both is qs[32c + 8o, +8).
-// y += d8 * d * sc * C - dmin * m * (d8 * sum(q8)). vecdotq.cuh:328-351; scale packing
-// gguf-py quants.py:480-502.
+// y += d8 * d * sc * C - dmin * m * t, t = d8 * sum(q8) (decode, vecdotq.cuh:328-351) or
+// y += d8 * half(d * sc) * C - half(dmin * m) * s8 with the stored sum s8 (batched, GGML
+// MMQ's load_tiles_q4_K and its tensor-core dot). Scale packing gguf-py quants.py:480-502.
 template <> struct MmqW<Q4_K> {
     static constexpr int SB = 144, NTERM = 8;
-    static constexpr bool SPLIT16 = false;
     struct Raw {
         uint4 hdr;
         uint2 q[4];
     };
-    static __device__ void load(Raw &r, const uint8_t *p, int o) {
+    static __device__ void load(Raw &r, const uint8_t *p, int o, int) {  // whole superblocks: no short step
         r.hdr = load_unaligned<uint4>(p);
 #pragma unroll
         for (int c = 0; c < 4; ++c) r.q[c] = load_unaligned<uint2>(p + 16 + 32 * c + 8 * o);
     }
-    static __device__ uint64_t codes(const Raw &r, int b, int, const uint32_t *) {
+    template <bool MMA> static constexpr int mode() { return MMQ_BLOCK; }
+    template <bool MMA> static __device__ uint64_t codes(const Raw &r, int b, int, const uint32_t *) {
         const uint64_t q = u64(r.q[b / 2]);
         return ((b & 1) ? q >> 4 : q) & 0x0f0f0f0f0f0f0f0full;
     }
-    static __device__ float scale(const Raw &r, int b) {
+    template <bool MMA> static __device__ float scale(const Raw &r, int b) {
         const float d = half_bits_to_float(r.hdr.x & 0xffffu);
         const uint32_t sc = b < 4 ? bits(r.hdr.y, 8 * b, 6)
                                   : bits(r.hdr.w, 8 * (b - 4), 4) | (bits(r.hdr.y, 8 * (b - 4) + 6, 2) << 4);
-        return d * static_cast<float>(sc);
+        const float v = d * static_cast<float>(sc);  // exact: 11 x 6 bits
+        return MMA ? half_round(v) : v;
     }
-    static __device__ float term(const Raw &r, int j, int o) {  // block 4j + o: -dmin * m
+    template <bool MMA> static __device__ float term(const Raw &r, int j, int o) {  // block 4j + o: -dmin * m
         const float dmin = half_bits_to_float(r.hdr.x >> 16);
         const uint32_t mn = j == 0 ? bits(r.hdr.z, 8 * o, 6)
                                    : bits(r.hdr.w, 8 * o + 4, 4) | (bits(r.hdr.z, 8 * o + 6, 2) << 4);
-        return -dmin * static_cast<float>(mn);
+        const float v = dmin * static_cast<float>(mn);
+        return -(MMA ? half_round(v) : v);
     }
 };
 
@@ -120,14 +137,13 @@ template <> struct MmqW<Q4_K> {
 // gguf-py quants.py:553-573.
 template <> struct MmqW<Q6_K> {
     static constexpr int SB = 210, NTERM = 0;
-    static constexpr bool SPLIT16 = true;
     struct Raw {
         uint2 ql[4];
         uint2 qh[2];
         uint4 sc;
         uint32_t d;
     };
-    static __device__ void load(Raw &r, const uint8_t *p, int o) {
+    static __device__ void load(Raw &r, const uint8_t *p, int o, int) {  // whole superblocks: no short step
 #pragma unroll
         for (int i = 0; i < 4; ++i) r.ql[i] = load_unaligned<uint2>(p + 64 * (i / 2) + 32 * (i % 2) + 8 * o);
 #pragma unroll
@@ -135,7 +151,7 @@ template <> struct MmqW<Q6_K> {
         r.sc = load_unaligned<uint4>(p + 192);
         r.d = load_unaligned<uint16_t>(p + 208);
     }
-    static __device__ uint64_t codes(const Raw &r, int b, int, const uint32_t *) {
+    template <bool MMA> static __device__ uint64_t codes(const Raw &r, int b, int, const uint32_t *) {
         const int h = b / 4, s = b % 4;
         const uint64_t ql = u64(r.ql[2 * h + (s & 1)]), qh = u64(r.qh[h]);
         const uint64_t c = ((ql >> (4 * (s >> 1))) & 0x0f0f0f0f0f0f0f0full) | (((qh >> (2 * s)) & 0x0303030303030303ull) << 4);
@@ -148,40 +164,50 @@ template <> struct MmqW<Q6_K> {
         const uint32_t w = g < 4 ? r.sc.x : g < 8 ? r.sc.y : g < 12 ? r.sc.z : r.sc.w;
         return static_cast<int8_t>(bits(w, 8 * (g % 4), 8));
     }
-    static __device__ float scale(const Raw &r, int) { return half_bits_to_float(r.d); }
-    static __device__ float term(const Raw &, int, int) { return 0.0f; }
+    template <bool MMA> static constexpr int mode() { return MMQ_ISPLIT; }
+    template <bool MMA> static __device__ float scale(const Raw &r, int) { return half_bits_to_float(r.d); }
+    template <bool MMA> static __device__ float term(const Raw &, int, int) { return 0.0f; }
 };
 
 // Q2_K superblock: scales[16] (low nibble scale, high nibble min, per 16 values),
-// qs[64], d, dmin. Block kb = 4h + s: code (qs[32h + v] >> 2s) & 3, multiplied by its
-// 4-bit scale (<= 45, no int8 overflow) so one MFMA covers both 16-value groups;
-// y += d8 * d * C' - dmin * (m_lo * d8 S_lo + m_hi * d8 S_hi). vecdotq.cuh:204-230;
-// layout gguf-py quants.py:407-429.
+// qs[64], d, dmin. Block kb = 4h + s: code (qs[32h + v] >> 2s) & 3.
+// Decode (vecdotq.cuh:204-230): the code times its 4-bit scale (<= 45, no int8 overflow)
+// so one MFMA covers both 16-value groups; y += d8 * d * C' - dmin * (m_lo t_lo + m_hi t_hi),
+// t = d8 * sum(q8) per 16 values.
+// Batched (GGML MMQ's load_tiles_q2_K and tensor-core dot): raw codes, one MFMA per
+// 16-value half with its own fp32 scale half(d * sc); y += d8 * (half(d sc_lo) C_lo +
+// half(d sc_hi) C_hi) - half(dmin m_lo) S_lo - half(dmin m_hi) S_hi, S the D2S6 sums.
+// Layout gguf-py quants.py:407-429.
 template <> struct MmqW<Q2_K> {
     static constexpr int SB = 84, NTERM = 16;
-    static constexpr bool SPLIT16 = false;
     struct Raw {
         uint4 sc;
         uint2 q[2];
         uint32_t dm;
     };
-    static __device__ void load(Raw &r, const uint8_t *p, int o) {
+    static __device__ void load(Raw &r, const uint8_t *p, int o, int) {  // whole superblocks: no short step
         r.sc = load_unaligned<uint4>(p);
 #pragma unroll
         for (int h = 0; h < 2; ++h) r.q[h] = load_unaligned<uint2>(p + 16 + 32 * h + 8 * o);
         r.dm = load_unaligned<uint32_t>(p + 80);
     }
     static __device__ uint32_t word(const Raw &r, int i) { return i == 0 ? r.sc.x : i == 1 ? r.sc.y : i == 2 ? r.sc.z : r.sc.w; }
-    static __device__ uint64_t codes(const Raw &r, int b, int o, const uint32_t *) {
+    template <bool MMA> static constexpr int mode() { return MMA ? MMQ_FSPLIT : MMQ_BLOCK; }
+    template <bool MMA> static __device__ uint64_t codes(const Raw &r, int b, int o, const uint32_t *) {
         const int h = b / 4, s = b % 4;
         const uint64_t q = (u64(r.q[h]) >> (2 * s)) & 0x0303030303030303ull;
+        if constexpr (MMA) return q;
         // scale byte 2b + (o >> 1) lies in word b / 2
         const uint32_t sc = bits(word(r, b / 2), 8 * (2 * (b & 1) + (o >> 1)), 4);
         return q * sc;
     }
-    static __device__ float scale(const Raw &r, int) { return half_bits_to_float(r.dm & 0xffffu); }
-    static __device__ float term(const Raw &r, int j, int o) {  // 16-value group 4j + o: -dmin * m
-        return -half_bits_to_float(r.dm >> 16) * static_cast<float>(bits(word(r, j), 8 * o + 4, 4));
+    template <bool MMA> static __device__ float scale(const Raw &r, int) { return half_bits_to_float(r.dm & 0xffffu); }
+    static __device__ float fscale(const Raw &r, int g) {  // batched: half(d * sc) of 16-value group g
+        return half_round(half_bits_to_float(r.dm & 0xffffu) * static_cast<float>(bits(word(r, g / 4), 8 * (g % 4), 4)));
+    }
+    template <bool MMA> static __device__ float term(const Raw &r, int j, int o) {  // 16-value group 4j + o: -dmin * m
+        const float v = half_bits_to_float(r.dm >> 16) * static_cast<float>(bits(word(r, j), 8 * o + 4, 4));
+        return -(MMA ? half_round(v) : v);
     }
 };
 
@@ -191,7 +217,6 @@ template <> struct MmqW<Q2_K> {
 // quants.py:1097-1125.
 template <> struct MmqW<IQ3_S> {
     static constexpr int SB = 110, NTERM = 0;
-    static constexpr bool SPLIT16 = false;
     struct Raw {
         uint32_t qs[8];
         uint32_t sg[8];
@@ -199,7 +224,7 @@ template <> struct MmqW<IQ3_S> {
         uint32_t sc;
         uint32_t d;
     };
-    static __device__ void load(Raw &r, const uint8_t *p, int o) {
+    static __device__ void load(Raw &r, const uint8_t *p, int o, int) {  // whole superblocks: no short step
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
             r.qs[b] = load_unaligned<uint16_t>(p + 2 + 8 * b + 2 * o);
@@ -209,17 +234,18 @@ template <> struct MmqW<IQ3_S> {
         r.sc = load_unaligned<uint32_t>(p + 106);
         r.d = load_unaligned<uint16_t>(p);
     }
-    static __device__ uint64_t codes(const Raw &r, int b, int o, const uint32_t *grid) {
+    template <bool MMA> static constexpr int mode() { return MMQ_BLOCK; }
+    template <bool MMA> static __device__ uint64_t codes(const Raw &r, int b, int o, const uint32_t *grid) {
         const uint32_t qh = bits(b < 4 ? r.qh.x : r.qh.y, 8 * (b % 4), 8) >> (2 * o);
         const uint32_t i0 = (r.qs[b] & 0xffu) | ((qh & 1u) << 8);
         const uint32_t i1 = (r.qs[b] >> 8) | ((qh & 2u) << 7);
         return uint64_t(Unit<IQ3_S>::signed_levels(grid[i0], r.sg[b] & 0x0fu)) |
                (uint64_t(Unit<IQ3_S>::signed_levels(grid[i1], r.sg[b] >> 4)) << 32);
     }
-    static __device__ float scale(const Raw &r, int b) {
+    template <bool MMA> static __device__ float scale(const Raw &r, int b) {
         return half_bits_to_float(r.d) * static_cast<float>(1 + 2 * static_cast<int>(bits(r.sc, 4 * b, 4)));
     }
-    static __device__ float term(const Raw &, int, int) { return 0.0f; }
+    template <bool MMA> static __device__ float term(const Raw &, int, int) { return 0.0f; }
 };
 
 

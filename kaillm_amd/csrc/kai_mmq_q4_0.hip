@@ -2,6 +2,8 @@
 #include "kai_mmq.cuh"
 
 namespace kai {
-template void launch_mmq_type<Q4_0>(const void *, int64_t, int64_t, int64_t, const block_q8_1 *, const float *, void *,
-                                  bool, int64_t, hipStream_t);
+template void launch_mmq_type<Q4_0, false>(const void *, int64_t, int64_t, int64_t, const void *, const float *, void *,
+                                       bool, int64_t, hipStream_t);
+template void launch_mmq_type<Q4_0, true>(const void *, int64_t, int64_t, int64_t, const void *, const float *, void *,
+                                      bool, int64_t, hipStream_t);
 }  // namespace kai

@@ -246,13 +246,9 @@ static void launch_sets(const uint8_t *w, int64_t n, int64_t k, const block_q8_1
     if (lds + (TYPE == IQ3_S ? 2048 : 0) + 64 > size_t(MMVQ_LDS_BUDGET))
         throw Error("GEMV activation does not fit in LDS (m * k too large)");
     auto kernel = mmvq_kernel<TYPE, M, TWO_PASS, DEPTH, G, RS>;
-    static bool attribute_set = false;  // per instantiation; raises the dynamic LDS limit once
-    if (!attribute_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                MMVQ_LDS_BUDGET - 4096) != hipSuccess)
-            throw Error("Cannot raise the GEMV dynamic LDS limit");
-        attribute_set = true;
-    }
+    static DeviceFlags lds_raised;  // per instantiation and device
+    raise_dynamic_lds(reinterpret_cast<const void *>(kernel), MMVQ_LDS_BUDGET - 4096, lds_raised,
+                      "Cannot raise the GEMV dynamic LDS limit");
     kernel<<<dim3(static_cast<unsigned>((n + rows_per_block - 1) / rows_per_block)), dim3(THREADS), lds, stream>>>(
         w, row_bytes, static_cast<int>(n), units, y1, y2, static_cast<int>(k / QK8_1), inverse, dst, stride_dst,
         dst_bf16 ? 1 : 0);

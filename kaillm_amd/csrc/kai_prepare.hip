@@ -187,75 +187,103 @@ __global__ __launch_bounds__(PREP_THREADS) void prepare_q8_1_kernel(
     }
 }
 
-// Min-term operands of one activation row, from t = d8 * sum(q8) (exact in fp32) and
-// u = sum(half(d8 q8) - d8 q8) over G values, hi = half(t), lo = half(t - hi):
-// G = 32 (t32): per superblock 4 block pairs of 8 fp16 [hi hi' lo lo' hi hi' u u'] (64
-// bytes), matching the weight operand [e_hi e_hi' e_hi e_hi' e_lo e_lo' f f'];
-// G = 16 (t16): per superblock three runs of 16 fp16 [hi | lo | u] (96 bytes).
+// ---------------------------------------------------------------- batched path (m > 8)
+// GGML MMQ quantisation of the normalised row (quantize_scaled,
+// current_ggml_direct.cu:1025-1092), per group of G values (G = 32: one quad; G = 64: two
+// quads, joined by one lane exchange): amax = max|v|, d_inv = 127 / amax,
+// q = roundf(v * d_inv) (NaN -> 0, saturated to int8: the reference's char conversion),
+// d = 1 / d_inv. Both divisions are IEEE (correctly rounded). Returns d; q and the lane's
+// code sum are written.
+__device__ __forceinline__ int mmq_code(float p) {
+    const float r = fminf(fmaxf(roundf(p), -128.0f), 127.0f);
+    return p != p ? 0 : static_cast<int>(r);
+}
 template <int G>
-__device__ __forceinline__ void store_min_operands(uint8_t *sb_base, int slot, float t, float u) {
-    uint16_t *h = reinterpret_cast<uint16_t *>(sb_base);
-    const uint16_t hi = float_to_half_bits(t);
-    const uint16_t lo = float_to_half_bits(t - half_bits_to_float(hi));
-    if constexpr (G == 32) {
-        uint16_t *pair = h + 8 * (slot / 2) + slot % 2;
-        pair[0] = hi;
-        pair[2] = lo;
-        pair[4] = hi;
-        pair[6] = float_to_half_bits(u);
-    } else {
-        h[slot] = hi;
-        h[16 + slot] = lo;
-        h[32 + slot] = float_to_half_bits(u);
+__device__ __forceinline__ float mmq_group_codes(const float (&v)[8], int8_t (&q)[8], int &lane_sum) {
+    float a = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(v[j]));
+    a = quad_max(a);
+    if constexpr (G == 64) a = fmaxf(a, __shfl_xor(a, 4, WAVE));
+    const float d_inv = 127.0f / a;
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int c = mmq_code(v[j] * d_inv);
+        q[j] = static_cast<int8_t>(c);
+        s += c;
     }
+    lane_sum = s;
+    return 1.0f / d_inv;
+}
+// fp16 bits of d * s, the product rounded to fp32 first (no fused conversion).
+__device__ __forceinline__ uint32_t half_of_product(float d, int s) {
+    float prod = d * static_cast<float>(s);
+    __asm__ volatile("" : "+v"(prod));
+    return float_to_half_bits(prod);
+}
+__device__ __forceinline__ uint2 pack_codes(const int8_t (&q)[8]) {
+    uint32_t w[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        w[i] = static_cast<uint32_t>(static_cast<uint8_t>(q[4 * i])) |
+               (static_cast<uint32_t>(static_cast<uint8_t>(q[4 * i + 1])) << 8) |
+               (static_cast<uint32_t>(static_cast<uint8_t>(q[4 * i + 2])) << 16) |
+               (static_cast<uint32_t>(static_cast<uint8_t>(q[4 * i + 3])) << 24);
+    return make_uint2(w[0], w[1]);
 }
 
-// Operands of the fp16-MFMA GEMMs (kai_mmf.cuh, kai_mfv.cuh): the row scale and Q8_1 codes
-// of prepare_q8_1_kernel (same arithmetic, same launch shape), written as
-// a16 = half(d8 * q8) with d8 the block's fp16 scale, plus the min-term operands of
-// 32-value sums (t32, 64 bytes per superblock) and of 16-value sums (t16, 96 bytes) when
-// those pointers are set. K is a multiple of 256.
+// Activation planes of the batched path: 128-value blocks of 144 bytes
+// (block_q8_1_mmq: 16 header bytes, int8 qs[128]) in [K/128][m] order, K padded to
+// MMQ_ROW_PADDING with zero blocks; the header per layout is
+//   D4   fp32 d of each 32 values;
+//   DS4  half2 (d, d * sum q) of each 32 values;
+//   D2S6 half d of each 64 values, then half d * sum q of the 16-value groups 0..5.
+// The row scale and inverse are those of prepare_q8_1_kernel (same launch shape, same
+// arithmetic), and one launch writes every plane the group needs (null when absent).
 template <int DTYPE>
-__global__ __launch_bounds__(PREP_THREADS) void prepare_mmf_kernel(
-    const typename Src<DTYPE>::T *__restrict__ x, int64_t stride_x, int k, uint16_t *__restrict__ a16,
-    uint8_t *__restrict__ t32, uint8_t *__restrict__ t16, float *__restrict__ inverse) {
+__global__ __launch_bounds__(PREP_THREADS) void prepare_mmq_kernel(
+    const typename Src<DTYPE>::T *__restrict__ x, int64_t stride_x, int k, int m, int kpad_blocks, MmqPlanes p) {
     __shared__ float wave_max_lds[PREP_THREADS / WAVE];
     const int row = blockIdx.x;
     const int nblocks = k / QK8_1;
     const int part = threadIdx.x & 3, ib = blockIdx.y * PREP_BLOCKS + (threadIdx.x >> 2);
     const auto *xr = x + static_cast<int64_t>(row) * stride_x;
     float v[8];
-    const float scale = row_scale<DTYPE>(xr, k, wave_max_lds, inverse + row, blockIdx.y == 0 && threadIdx.x == 0, v);
-    if (ib >= nblocks) return;  // whole quads
+    const float scale = row_scale<DTYPE>(xr, k, wave_max_lds, p.inverse + row, blockIdx.y == 0 && threadIdx.x == 0, v);
+    if (ib >= kpad_blocks) return;  // whole groups of 8 lanes (kpad_blocks is a multiple of 16)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] *= scale;
-    int8_t q[8];
-    const BlockCodes b = quad_codes(v, q);
-    const float d8 = half_bits_to_float(b.hd);
-    uint32_t words[4];
-    float u = 0.0f;
-    int s = 0;
-#pragma unroll
-    for (int j = 0; j < 8; j += 2) {
-        const float e0 = d8 * static_cast<float>(q[j]), e1 = d8 * static_cast<float>(q[j + 1]);  // exact
-        const uint16_t h0 = float_to_half_bits(e0), h1 = float_to_half_bits(e1);
-        u += (half_bits_to_float(h0) - e0) + (half_bits_to_float(h1) - e1);
-        s += q[j] + q[j + 1];
-        words[j / 2] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+    for (int j = 0; j < 8; ++j) v[j] = ib < nblocks ? v[j] * scale : 0.0f;
+    const int sub = ib & 3;  // 32-value block within the 128-value block
+    const size_t blk = (static_cast<size_t>(ib >> 2) * static_cast<size_t>(m) + static_cast<size_t>(row)) * MMQ_BLOCK_BYTES;
+    const size_t codes = blk + 16 + 32 * sub + 8 * part;
+    if (p.d4 || p.ds4) {
+        int8_t q[8];
+        int s;
+        const float d = mmq_group_codes<32>(v, q, s);
+        const uint2 packed = pack_codes(q);
+        if (p.d4) {
+            *reinterpret_cast<uint2 *>(p.d4 + codes) = packed;
+            if (part == 0) *reinterpret_cast<float *>(p.d4 + blk + 4 * sub) = d;
+        }
+        if (p.ds4) {
+            *reinterpret_cast<uint2 *>(p.ds4 + codes) = packed;
+            const int total = quad_sum(s);
+            if (part == 0)
+                *reinterpret_cast<uint32_t *>(p.ds4 + blk + 4 * sub) =
+                    static_cast<uint32_t>(float_to_half_bits(d)) | (half_of_product(d, total) << 16);
+        }
     }
-    // Runs of 8 values go to their place in the superblock's K order (mmf_a16_run).
-    uint4 *dst = reinterpret_cast<uint4 *>(a16 + static_cast<int64_t>(row) * k + static_cast<int64_t>(ib / 8) * 256);
-    dst[mmf_a16_run(ib % 8, part)] = make_uint4(words[0], words[1], words[2], words[3]);
-    const int64_t sb = static_cast<int64_t>(row) * (k / 256) + ib / 8;
-    if (t32) {
-        const float ub = quad_sum(u);
-        if (part == 0) store_min_operands<32>(t32 + sb * 64, ib % 8, d8 * static_cast<float>(b.isum), ub);
-    }
-    if (t16) {  // 16-value halves: parts 0-1 and 2-3
-        const int s16 = s + dpp_i32<DPP_QUAD_1032>(s);
-        const float u16 = u + dpp_f32<DPP_QUAD_1032>(u);
-        if ((part & 1) == 0)
-            store_min_operands<16>(t16 + sb * 96, 2 * (ib % 8) + part / 2, d8 * static_cast<float>(s16), u16);
+    if (p.d2s6) {
+        int8_t q[8];
+        int s;
+        const float d = mmq_group_codes<64>(v, q, s);
+        *reinterpret_cast<uint2 *>(p.d2s6 + codes) = pack_codes(q);
+        const int s16 = s + dpp_i32<DPP_QUAD_1032>(s);  // lanes {0,1} and {2,3}: 16 values each
+        const int slot = 2 * sub + (part >> 1);
+        uint16_t *hdr = reinterpret_cast<uint16_t *>(p.d2s6 + blk);
+        if ((part & 1) == 0 && slot < 6) hdr[2 + slot] = static_cast<uint16_t>(half_of_product(d, s16));
+        if ((sub & 1) == 0 && part == 0) hdr[sub >> 1] = float_to_half_bits(d);
     }
 }
 
@@ -285,31 +313,25 @@ void launch_prepare(const void *x, int x_dtype, int64_t m, int64_t k, int64_t st
     }
 }
 
-void launch_prepare_mmf(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const MmfAct &out,
+template <int DTYPE>
+static void launch_prepare_mmq_dtype(const void *x, int64_t m, int64_t k, int64_t stride_x, const MmqPlanes &p,
+                                     hipStream_t stream) {
+    const int kpad_blocks = static_cast<int>(mmq_blocks128(k) * 4);
+    const dim3 grid(static_cast<unsigned>(m), static_cast<unsigned>((kpad_blocks + PREP_BLOCKS - 1) / PREP_BLOCKS));
+    prepare_mmq_kernel<DTYPE><<<grid, dim3(PREP_THREADS), 0, stream>>>(
+        static_cast<const typename Src<DTYPE>::T *>(x), stride_x, static_cast<int>(k), static_cast<int>(m),
+        kpad_blocks, p);
+}
+
+void launch_prepare_mmq(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const MmqPlanes &planes,
                         hipStream_t stream) {
-    if (k / QK8_1 > PREP_MAX_BLOCKS) throw Error("Fused activation preparation supports K <= 32768");
-    if (k % 256) throw Error("The fp16-MFMA GEMM needs K to be a multiple of 256");
-    const int nblocks = static_cast<int>(k / QK8_1);
-    const dim3 grid(static_cast<unsigned>(m), static_cast<unsigned>((nblocks + PREP_BLOCKS - 1) / PREP_BLOCKS)),
-        block(PREP_THREADS);
-    const int kk = static_cast<int>(k);
+    if (k % QK8_1 || k <= 0 || m <= 0 || m > INT_MAX || mmq_blocks128(k) * 4 > INT_MAX)
+        throw Error("Invalid batched activation shape");
     switch (x_dtype) {
-        case 0:
-            prepare_mmf_kernel<0><<<grid, block, 0, stream>>>(static_cast<const float *>(x), stride_x, kk, out.a16,
-                                                               out.t32, out.t16, out.inverse);
-            break;
-        case 1:
-        case 2: {
-            const auto *src = static_cast<const uint16_t *>(x);
-            if (x_dtype == 1)
-                prepare_mmf_kernel<1><<<grid, block, 0, stream>>>(src, stride_x, kk, out.a16, out.t32, out.t16,
-                                                                   out.inverse);
-            else
-                prepare_mmf_kernel<2><<<grid, block, 0, stream>>>(src, stride_x, kk, out.a16, out.t32, out.t16,
-                                                                   out.inverse);
-            break;
-        }
-        default: throw Error("Fused activations must be F32, BF16 or F16");
+        case 0: launch_prepare_mmq_dtype<0>(x, m, k, stride_x, planes, stream); break;
+        case 1: launch_prepare_mmq_dtype<1>(x, m, k, stride_x, planes, stream); break;
+        case 2: launch_prepare_mmq_dtype<2>(x, m, k, stride_x, planes, stream); break;
+        default: throw Error("Fused MMQ activations must be F32, BF16 or F16");
     }
 }
 

@@ -574,6 +574,240 @@ int oracle_mul_mat_f32(int type, const uint8_t *weight, int64_t n, int64_t k, in
     return 0;
 }
 
+/* ---------------------------------------------------------------- batched path (m > 8) */
+
+#define MMQ_BLOCK_BYTES 144 /* block_q8_1_mmq: 16 header bytes + 128 codes */
+#define MMQ_ROW_PADDING 512 /* MATRIX_ROW_PADDING, current_ggml_direct.cu:1136 */
+
+/* Layout per type: GGML's mmq_get_q8_1_ds_layout (upstream mmq.cuh), as selected per
+ * matrix by layout_index (current_ggml_direct.cu:1113-1116). */
+int oracle_mmq_layout(int type) {
+    switch (type) {
+        case ORACLE_Q8_0: case ORACLE_Q6_K: case ORACLE_IQ3_S: return ORACLE_MMQ_D4;
+        case ORACLE_Q4_0: case ORACLE_Q4_K: return ORACLE_MMQ_DS4;
+        case ORACLE_Q2_K: return ORACLE_MMQ_D2S6;
+        default: return -1;
+    }
+}
+
+int64_t oracle_mmq_blocks128(int64_t k) {
+    return (k + MMQ_ROW_PADDING - 1) / MMQ_ROW_PADDING * (MMQ_ROW_PADDING / 128);
+}
+
+size_t oracle_mmq_plane_bytes(int64_t m, int64_t k) {
+    return (size_t)oracle_mmq_blocks128(k) * (size_t)m * MMQ_BLOCK_BYTES;
+}
+
+/* Row scale of row_scale (current_ggml_direct.cu:978-1022): the same closed form as the
+ * decode preparation (kai_dual_mmvq.cuh:202-211). Returns scale, writes inverse. */
+static float mmq_row_scale(const void *x, int x_dtype, int64_t row_off, int64_t k, float *inverse) {
+    float amax = 0.0f;
+    for (int64_t i = 0; i < k; ++i) amax = fmaxf(amax, fabsf(load_x(x, x_dtype, row_off + i)));
+    const int biased = (int)((f2u(amax) >> 23) & 255u);
+    int se = 127;
+    if (biased != 0 && biased != 255) {
+        se = 260 - biased;
+        if (se < 1) se = 1;
+        if (se > 253) se = 253;
+    }
+    *inverse = u2f((uint32_t)(254 - se) << 23);
+    return u2f((uint32_t)se << 23);
+}
+
+/* float -> int8 as the reference's char4 store of roundf(...) converts it: NaN to 0,
+ * out-of-range saturated (only reachable when d_inv overflows to inf). */
+static int8_t mmq_code(float p) {
+    if (p != p) return 0;
+    const float r = roundf(p);
+    if (r > 127.0f) return 127;
+    if (r < -128.0f) return -128;
+    return (int8_t)r;
+}
+
+/*
+ * quantize_scaled (current_ggml_direct.cu:1025-1092) over one row, normalised values v
+ * (zero past k). Per G-value group (G = 64 for D2S6, else 32): amax = fmaxf over |v|
+ * (:1045-1052), d_inv = 127/amax (:1053), q = roundf(v*d_inv) (:1054-1058), d = 1/d_inv
+ * (:1059); sums d*float(sum q) over 32 (DS4) or 16 (D2S6) values (:1061-1068); stores
+ * (:1070-1090): D4 d4[i/32] = d; DS4 ds4[i/32] = half2_rn(d, sum); D2S6 d2s6[i/64] = half(d),
+ * d2s6[2 + i/16] = half(sum) for i < 96.
+ */
+static void mmq_quantize_row(const float *v, int64_t kpad, int layout, int64_t m, int64_t row, uint8_t *plane) {
+    const int g = layout == ORACLE_MMQ_D2S6 ? 64 : 32;
+    for (int64_t b = 0; b < kpad / 128; ++b) {
+        uint8_t *blk = plane + ((size_t)b * (size_t)m + (size_t)row) * MMQ_BLOCK_BYTES;
+        int8_t *qs = (int8_t *)(blk + 16);
+        for (int gi = 0; gi < 128 / g; ++gi) {
+            const float *vg = v + b * 128 + gi * g;
+            float amax = 0.0f;
+            for (int i = 0; i < g; ++i) amax = fmaxf(amax, fabsf(vg[i]));
+            const float d_inv = 127.0f / amax;
+            const float d = 1.0f / d_inv;
+            int8_t *q = qs + gi * g;
+            for (int i = 0; i < g; ++i) q[i] = mmq_code(vg[i] * d_inv);
+            if (layout == ORACLE_MMQ_D4) {
+                memcpy(blk + 4 * gi, &d, 4);
+            } else if (layout == ORACLE_MMQ_DS4) {
+                int s = 0;
+                for (int i = 0; i < 32; ++i) s += q[i];
+                const uint16_t hd = oracle_float_to_half(d), hs = oracle_float_to_half(d * (float)s);
+                memcpy(blk + 4 * gi, &hd, 2);
+                memcpy(blk + 4 * gi + 2, &hs, 2);
+            } else {
+                const uint16_t hd = oracle_float_to_half(d);
+                memcpy(blk + 2 * gi, &hd, 2);
+                for (int h = 0; h < 4; ++h) {
+                    const int slot = 4 * gi + h; /* 16-value group within the 128 */
+                    if (slot >= 6) continue;
+                    int s = 0;
+                    for (int i = 0; i < 16; ++i) s += q[16 * h + i];
+                    const uint16_t hs = oracle_float_to_half(d * (float)s);
+                    memcpy(blk + 4 + 2 * slot, &hs, 2);
+                }
+            }
+        }
+    }
+}
+
+int oracle_prepare_mmq(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x,
+                       int layout, uint8_t *plane, float *inverse) {
+    if (!x || !plane || !inverse || m < 1 || k <= 0 || k % 4 || stride_x < k || x_dtype < 0 || x_dtype > 2 ||
+        layout < 0 || layout > 2)
+        return -1;
+    const int64_t kpad = oracle_mmq_blocks128(k) * 128;
+    float *v = (float *)malloc((size_t)kpad * sizeof(float));
+    if (!v) return -1;
+    for (int64_t row = 0; row < m; ++row) {
+        const float scale = mmq_row_scale(x, x_dtype, row * stride_x, k, inverse + row);
+        for (int64_t i = 0; i < kpad; ++i) v[i] = i < k ? load_x(x, x_dtype, row * stride_x + i) * scale : 0.0f;
+        mmq_quantize_row(v, kpad, layout, m, row, plane);
+    }
+    free(v);
+    return 0;
+}
+
+static float h2f_bits(const uint8_t *p) { return rd_half(p); }
+static double half_round(double v) { return (double)oracle_half_to_float(oracle_float_to_half((float)v)); }
+
+/*
+ * One weight block against its activation in a plane (row j of m), FP64 from exact
+ * integer dots. GGML MMQ (upstream mmq.cuh @0c1e570, not vendored) on int8 tensor cores,
+ * restated from its published tile loaders and dots:
+ *   Q8_0  (D4)   d_w * d4 * sum q_w q                      load_tiles_q8_0, vec_dot_q8_0_q8_1_mma
+ *   Q4_0  (DS4)  d_w * d8 * sum (nib - 8) q                 load_tiles_q4_0 (codes - 8), same dot on ds.x
+ *   Q4_K  (DS4)  sum_i half(d sc_i) d8_i dot_i - half(dmin m_i) s8_i
+ *                                                           load_tiles_q4_K (x_dm = dm*(sc, m) in half),
+ *                                                           vec_dot_q8_1_q8_1_mma (s8 = stored ds.y)
+ *   Q6_K  (D4)   d * sum_i d4_i (sc_2i dot_2i + sc_2i+1 dot_2i+1)   vec_dot_q6_K_q8_1_mma
+ *   Q2_K  (D2S6) sum_g half(d sc_g) d64 dot_g - half(dmin m_g) S_g with S_g the stored half
+ *                sum for the first 96 values of a 128-block and d64 * sum q for the last 32
+ *                                                           load_tiles_q2_K, vec_dot_q2_K_q8_1_mma
+ *   IQ3_S (D4)   sum_i d (1 + 2 sc_i) d4_i dot_i            load_tiles_iq3_s, vec_dot_q8_0_q8_1_mma
+ * The value formulas are those of vecdotq.cuh (cited at block_dot); only the activation's
+ * scales and sums and the half rounding of the K-quant weight scales differ.
+ */
+static double mmq_block_dot(int type, const uint8_t *b, const uint8_t *plane, int64_t m, int64_t j, int64_t e0) {
+    /* activation values [e0, e0 + qk) of row j: 128-block e/128, position e%128 */
+#define ABLK(e) (plane + ((size_t)((e) / 128) * (size_t)m + (size_t)j) * MMQ_BLOCK_BYTES)
+#define ACODE(e) (((const int8_t *)(ABLK(e) + 16))[(e) % 128])
+    switch (type) {
+        case ORACLE_Q8_0: {
+            float d4;
+            memcpy(&d4, ABLK(e0) + 4 * ((e0 % 128) / 32), 4);
+            int64_t s = 0;
+            for (int e = 0; e < 32; ++e) s += (int64_t)(int8_t)b[2 + e] * ACODE(e0 + e);
+            return (double)rd_half(b) * (double)d4 * (double)s;
+        }
+        case ORACLE_Q4_0: {
+            const double d8 = h2f_bits(ABLK(e0) + 4 * ((e0 % 128) / 32));
+            int64_t s = 0;
+            for (int e = 0; e < 16; ++e)
+                s += (int64_t)((b[2 + e] & 0x0f) - 8) * ACODE(e0 + e) + (int64_t)((b[2 + e] >> 4) - 8) * ACODE(e0 + e + 16);
+            return (double)rd_half(b) * d8 * (double)s;
+        }
+        case ORACLE_Q4_K: {
+            const float d = rd_half(b), dmin = rd_half(b + 2);
+            uint8_t sc[8], mn[8];
+            q4k_scale_min(b + 4, sc, mn);
+            double acc = 0.0;
+            for (int i = 0; i < 8; ++i) {
+                const int64_t e = e0 + 32 * i;
+                const uint8_t *hdr = ABLK(e) + 4 * ((e % 128) / 32);
+                const double d8 = h2f_bits(hdr), s8 = h2f_bits(hdr + 2);
+                int64_t dot = 0;
+                for (int l = 0; l < 32; ++l) dot += (int64_t)q4k_code(b, 32 * i + l) * ACODE(e + l);
+                acc += half_round((double)d * sc[i]) * d8 * (double)dot - half_round((double)dmin * mn[i]) * s8;
+            }
+            return acc;
+        }
+        case ORACLE_Q6_K: {
+            const double d = rd_half(b + 208);
+            double acc = 0.0;
+            for (int g = 0; g < 16; ++g) {
+                const int64_t e = e0 + 16 * g;
+                float d4;
+                memcpy(&d4, ABLK(e) + 4 * ((e % 128) / 32), 4);
+                int64_t dot = 0;
+                for (int l = 0; l < 16; ++l) dot += (int64_t)q6k_code(b, 16 * g + l) * ACODE(e + l);
+                acc += (double)d4 * (double)(int8_t)b[192 + g] * (double)dot;
+            }
+            return d * acc;
+        }
+        case ORACLE_Q2_K: {
+            const float d = rd_half(b + 80), dmin = rd_half(b + 82);
+            double acc = 0.0;
+            for (int g = 0; g < 16; ++g) {
+                const int64_t e = e0 + 16 * g;
+                const uint8_t *hdr = ABLK(e);
+                const int slot = (int)((e % 128) / 16);
+                const double d64 = h2f_bits(hdr + 2 * (slot / 4));
+                int64_t dot = 0, qsum = 0;
+                for (int l = 0; l < 16; ++l) {
+                    dot += (int64_t)q2k_code(b, 16 * g + l) * ACODE(e + l);
+                    qsum += ACODE(e + l);
+                }
+                const double s = slot < 6 ? (double)h2f_bits(hdr + 4 + 2 * slot) : d64 * (double)qsum;
+                acc += half_round((double)d * (b[g] & 0x0f)) * d64 * (double)dot - half_round((double)dmin * (b[g] >> 4)) * s;
+            }
+            return acc;
+        }
+        case ORACLE_IQ3_S: {
+            const double d = rd_half(b);
+            double acc = 0.0;
+            for (int g = 0; g < 8; ++g) {
+                const int64_t e = e0 + 32 * g;
+                float d4;
+                memcpy(&d4, ABLK(e) + 4 * ((e % 128) / 32), 4);
+                int64_t dot = 0;
+                for (int t = 0; t < 32; ++t) dot += (int64_t)iq3s_value(b, 32 * g + t) * ACODE(e + t);
+                acc += d * (double)(1 + 2 * iq3s_scale(b, g)) * (double)d4 * (double)dot;
+            }
+            return acc;
+        }
+        default: return 0.0;
+    }
+#undef ACODE
+#undef ABLK
+}
+
+int oracle_mul_mat_mmq(int type, const uint8_t *weight, int64_t n, int64_t k, int64_t m,
+                       const uint8_t *plane, const float *inverse, double *out, int threads) {
+    if (!mm_args_ok(type, n, k, m, weight, plane) || !inverse || !out || oracle_mmq_layout(type) < 0) return -1;
+    const int qk = oracle_block_elems(type), bb = oracle_block_bytes(type);
+    const int64_t row_bytes = (k / qk) * bb;
+    (void)threads;
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
+    for (int64_t r = 0; r < n; ++r) {
+        for (int64_t j = 0; j < m; ++j) {
+            double acc = 0.0;
+            for (int64_t blk = 0; blk < k / qk; ++blk)
+                acc += mmq_block_dot(type, weight + r * row_bytes + blk * bb, plane, m, j, blk * qk);
+            out[j * n + r] = (double)inverse[j] * acc;
+        }
+    }
+    return 0;
+}
+
 const char *oracle_build_info(void) {
 #ifdef _OPENMP
     return "kai_oracle C99 restatement, OpenMP";

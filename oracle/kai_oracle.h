@@ -16,6 +16,10 @@
  *     as exact integer block sums times the stored fp16 scales, accumulated in FP64;
  *   - the GEMV epilogue y[j, r] = inverse[j] * sum_b dot(W[r, b], q8[j, b])
  *     (kai_dual_mmvq.cuh:258-327);
+ *   - the batched path of kai_fused_mmq_run (current_ggml_direct.cu:967-1265): row_scale,
+ *     GGML's MMQ activation quantisation quantize_scaled with its D4 / DS4 / D2S6 layouts
+ *     (:978-1092), and GGML MMQ's block arithmetic per format (upstream ggml mmq.cuh
+ *     @0c1e570, not vendored: restated from its published tile loaders and MMA dots);
  *   - block dequantization per gguf-py quants.py (:242-252, :397-402, :407-429,
  *     :476-523, :553-573, :1097-1125);
  *   - the fused activation producers kai_dual::prepare_view / prepare_swiglu /
@@ -101,6 +105,36 @@ int oracle_mul_mat(int type, const uint8_t *weight, int64_t n, int64_t k, int64_
 int oracle_mul_mat_f32(int type, const uint8_t *weight, int64_t n, int64_t k, int64_t m,
                        const void *activation, int two_pass, float *out, int64_t stride_out,
                        int threads);
+
+/* ---- Batched path (kai_fused_mmq_run, more than 8 rows; current_ggml_direct.cu:967-1265).
+ *
+ * Activation: the same power-of-two row normalisation (row_scale, :978-1022), then GGML's
+ * MMQ quantisation of the normalised row (quantize_scaled, :1025-1092) into one "plane"
+ * per layout: 128-value blocks of 144 bytes {16 bytes of scales/sums; int8 qs[128]} in
+ * [K/128][m] order, K padded to a multiple of 512 with zero blocks (:1136). Per group of
+ * G values (G = 64 for D2S6, else 32): amax = max|v|, d_inv = 127/amax, q = roundf(v*d_inv)
+ * (NaN -> 0, saturated to int8), d = 1/d_inv. The 16 header bytes hold
+ *   D4   (Q8_0, Q6_K, IQ3_S): fp32 d per 32 values;
+ *   DS4  (Q4_0, Q4_K):        half2 (d, d*sum q) per 32 values;
+ *   D2S6 (Q2_K):              half d per 64 values (2), then half d*sum q per 16 values for
+ *                             the first 96 values (6); the last 32 carry no stored sum. */
+enum { ORACLE_MMQ_D4 = 0, ORACLE_MMQ_DS4 = 1, ORACLE_MMQ_D2S6 = 2 };
+
+/* Layout a weight type's MMQ reads (-1 if unsupported); 128-value blocks per row; bytes
+ * of one plane. */
+int oracle_mmq_layout(int type);
+int64_t oracle_mmq_blocks128(int64_t k);
+size_t oracle_mmq_plane_bytes(int64_t m, int64_t k);
+
+/* row_scale + quantize_scaled for one layout: writes inverse[m] and the plane. */
+int oracle_prepare_mmq(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x,
+                       int layout, uint8_t *plane, float *inverse);
+
+/* GGML MMQ over a plane of the type's layout, in FP64 from exact integer block dots:
+ * out[j * n + r] = inverse[j] * sum over blocks. Weight-side scales are those GGML's
+ * MMQ tile loaders form (half(d*sc), half(dmin*m) for Q4_K and Q2_K). */
+int oracle_mul_mat_mmq(int type, const uint8_t *weight, int64_t n, int64_t k, int64_t m,
+                       const uint8_t *plane, const float *inverse, double *out, int threads);
 
 /* Library identity string (build flags), for reports. */
 const char *oracle_build_info(void);

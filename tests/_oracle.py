@@ -50,6 +50,16 @@ def lib():
     o.oracle_norm_prepare.argtypes = [ptr, c_int, i64, ptr, c_int, i64, ptr, ptr, ctypes.c_float, ptr, i64, i64,
                                       ptr]
     o.oracle_norm_prepare.restype = c_int
+    o.oracle_mmq_layout.argtypes = [c_int]
+    o.oracle_mmq_layout.restype = c_int
+    o.oracle_mmq_blocks128.argtypes = [i64]
+    o.oracle_mmq_blocks128.restype = i64
+    o.oracle_mmq_plane_bytes.argtypes = [i64, i64]
+    o.oracle_mmq_plane_bytes.restype = ctypes.c_size_t
+    o.oracle_prepare_mmq.argtypes = [ptr, c_int, i64, i64, i64, c_int, ptr, ptr]
+    o.oracle_prepare_mmq.restype = c_int
+    o.oracle_mul_mat_mmq.argtypes = [c_int, ptr, i64, i64, i64, ptr, ptr, ptr, c_int]
+    o.oracle_mul_mat_mmq.restype = c_int
     o.oracle_build_info.restype = ctypes.c_char_p
     return o
 
@@ -188,3 +198,65 @@ def random_blocks(qtype, n, k, rng):
     elif qtype == IQ3_S:
         put_half(0, 0.0, 0.002)
     return w.reshape(n, nb * bb)
+
+
+# ----------------------------------------------------------------- batched path (m > 8)
+
+D4, DS4, D2S6 = 0, 1, 2
+LAYOUT_NAMES = {D4: "D4", DS4: "DS4", D2S6: "D2S6"}
+
+
+def mmq_layout(qtype):
+    return lib().oracle_mmq_layout(qtype)
+
+
+def mmq_blocks128(k):
+    return lib().oracle_mmq_blocks128(k)
+
+
+def prepare_mmq(x, layout, dtype_code=None):
+    """-> (plane uint8 [K/128 padded, m, 144], inverse f32 [m]) of the batched path."""
+    x = np.ascontiguousarray(x)
+    if dtype_code is None:
+        dtype_code = _code(x)
+    m, k = x.shape
+    plane = np.zeros(lib().oracle_mmq_plane_bytes(m, k), dtype=np.uint8)
+    inverse = np.zeros(m, dtype=np.float32)
+    assert lib().oracle_prepare_mmq(_p(x), dtype_code, m, k, k, layout, _p(plane), _p(inverse)) == 0
+    return plane.reshape(mmq_blocks128(k), m, 144), inverse
+
+
+def split_plane(plane, layout):
+    """-> (q int8 [m, Kpad], d [m, Kpad/G] f32, sums [m, Kpad/16 or Kpad/32] f32 or None).
+
+    sums: DS4 per 32 values; D2S6 per 16 values with NaN where no sum is stored."""
+    nb, m, _ = plane.shape
+    q = plane[:, :, 16:].copy().view(np.int8).transpose(1, 0, 2).reshape(m, nb * 128)
+    hdr = plane[:, :, :16].copy()
+    if layout == D4:
+        d = hdr.view(np.float32).reshape(nb, m, 4).transpose(1, 0, 2).reshape(m, nb * 4)
+        return q, d, None
+    h = hdr.view(np.float16).astype(np.float32).reshape(nb, m, 8).transpose(1, 0, 2)
+    if layout == DS4:
+        return q, h[:, :, 0::2].reshape(m, nb * 4), h[:, :, 1::2].reshape(m, nb * 4)
+    sums = np.full((m, nb, 8), np.nan, dtype=np.float32)
+    sums[:, :, :6] = h[:, :, 2:8]
+    return q, h[:, :, :2].reshape(m, nb * 2), sums.reshape(m, nb * 8)
+
+
+def mul_mat_mmq(qtype, w, k, plane, inverse, threads=8):
+    """Reference batched GEMM (GGML MMQ arithmetic) in FP64: out [m, n]."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    plane = np.ascontiguousarray(plane)
+    n = w.shape[0]
+    m = plane.shape[1]
+    out = np.empty((m, n), dtype=np.float64)
+    assert lib().oracle_mul_mat_mmq(qtype, _p(w), n, k, m, _p(plane), _p(inverse), _p(out), threads) == 0
+    return out
+
+
+def mmq_reference(qtype, w, x, dtype_code=None, threads=8):
+    """The batched path's result for x [m, k] (float32 / float16 / bf16 bits as uint16)."""
+    k = x.shape[1]
+    plane, inverse = prepare_mmq(x, mmq_layout(qtype), dtype_code)
+    return mul_mat_mmq(qtype, w, k, plane, inverse, threads)

@@ -1,0 +1,99 @@
+"""Parity at BASELINE.json's full shapes, through the C ABI.
+
+The GPU runs every product at its real size; the CPU oracle checks a seeded sample of
+output columns (weight rows), chosen to include the first and last rows of the matrix,
+so its cost stays bounded. Also covers the GEMV variants that only large matrices reach
+(two row sets per wave, from 8192 row sets on).
+"""
+import numpy as np
+import pytest
+import torch
+
+import _oracle as O
+from test_gpu_parity import TOL_F32, gpu_mmq, gpu_mmvq, gpu_prepare, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def sample_cols(n, rng, count=64):
+    edge = list(range(4)) + list(range(n - 4, n))
+    return np.unique(np.concatenate([edge, rng.choice(n, size=min(count, n), replace=False)]))
+
+
+def quantized(qtype, n, k, rng):
+    from kaillm_amd.formats import quantize
+    return quantize((rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)), qtype)
+
+
+# GEMV (kai_fused_mmvq) at 34816 x 5120: two row sets per wave for Q4_K at 1-4 rows and for
+# the other formats at 3-4 rows, up to each format's GEMV row limit (larger m goes to MMQ).
+TWO_SETS = [(O.Q4_K, 2), (O.Q4_K, 3), (O.Q4_K, 4), (O.Q2_K, 3), (O.IQ3_S, 3), (O.IQ3_S, 4),
+            (O.Q4_0, 3), (O.Q4_0, 4), (O.Q8_0, 3), (O.Q8_0, 4), (O.Q6_K, 3), (O.Q6_K, 4)]
+
+
+@pytest.mark.parametrize("qtype,m", TWO_SETS, ids=[f"{O.NAMES[t]}-m{m}" for t, m in TWO_SETS])
+def test_gemv_two_row_sets(kai, qtype, m):
+    n, k = 34816, 5120
+    print(f"gemv two row sets {O.NAMES[qtype]} {n}x{k} m={m}", flush=True)
+    rng = np.random.default_rng(qtype * 10 + m)
+    w = O.random_blocks(qtype, n, k, rng)
+    x = rng.standard_normal((m, k), dtype=np.float32).astype(np.float16)
+    out = gpu_mmvq(kai, qtype, to_dev(w), n, k, gpu_prepare(kai, to_dev(x)), m)
+    cols = sample_cols(n, rng)
+    ref = O.mul_mat(qtype, w[cols], k, O.prepare(x), m, threads=16)
+    err = O.normwise_rel(out[:, cols].cpu().numpy(), ref)
+    print(f"  normwise rel err {err:.3e}")
+    assert err <= TOL_F32
+
+
+# C2 (LFM-like Q4_0 decode) qkv at every batch, checked in full.
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
+def test_c2_qkv_decode(kai, m):
+    n, k = 3072, 2048
+    print(f"C2 Q4_0 qkv m={m}", flush=True)
+    rng = np.random.default_rng(300 + m)
+    w = quantized(O.Q4_0, n, k, rng)
+    x = rng.standard_normal((m, k), dtype=np.float32).astype(np.float16)
+    out = gpu_mmvq(kai, O.Q4_0, to_dev(w), n, k, gpu_prepare(kai, to_dev(x)), m)
+    ref = O.mul_mat(O.Q4_0, w, k, O.prepare(x), m, threads=16)
+    assert O.normwise_rel(out.cpu().numpy(), ref) <= TOL_F32
+
+
+# The batched path (kai_fused_mmq_run) at every BASELINE shape above 8 rows: C3 batch 16,
+# C4 spec-verify (80) and prefill (512, 2048), C5 batch 16 and prefill.
+BATCHED = [
+    ("C3 Q4_K gate/up b16", O.Q4_K, 34816, 5120, 16),
+    ("C3 Q4_K qkv b16", O.Q4_K, 7168, 5120, 16),
+    ("C3 Q6_K down b16", O.Q6_K, 5120, 17408, 16),
+    ("C3 Q6_K o_proj b16", O.Q6_K, 5120, 6144, 16),
+    ("C4 Q4_K gate/up M80", O.Q4_K, 34816, 5120, 80),
+    ("C4 Q4_K down M80", O.Q4_K, 5120, 17408, 80),
+    ("C4 Q4_K gate/up M512", O.Q4_K, 34816, 5120, 512),
+    ("C4 Q4_K down M512", O.Q4_K, 5120, 17408, 512),
+    ("C4 Q4_K gate/up M2048", O.Q4_K, 34816, 5120, 2048),
+    ("C4 Q4_K down M2048", O.Q4_K, 5120, 17408, 2048),
+    ("C5 Q2_K gate/up b16", O.Q2_K, 34816, 5120, 16),
+    ("C5 Q2_K down b16", O.Q2_K, 5120, 17408, 16),
+    ("C5 Q2_K gate/up M2048", O.Q2_K, 34816, 5120, 2048),
+    ("C5 Q2_K down M2048", O.Q2_K, 5120, 17408, 2048),
+    ("C5 IQ3_S gate/up b16", O.IQ3_S, 34816, 5120, 16),
+    ("C5 IQ3_S down b16", O.IQ3_S, 5120, 17408, 16),
+    ("C5 IQ3_S gate/up M2048", O.IQ3_S, 34816, 5120, 2048),
+    ("C5 IQ3_S down M2048", O.IQ3_S, 5120, 17408, 2048),
+]
+
+
+@pytest.mark.parametrize("name,qtype,n,k,m", BATCHED, ids=[b[0] for b in BATCHED])
+def test_batched_full_size(kai, name, qtype, n, k, m):
+    print(f"batched full size {name}", flush=True)
+    rng = np.random.default_rng(n + k + m + qtype)
+    w = quantized(qtype, n, k, rng)
+    x = rng.standard_normal((m, k), dtype=np.float32).astype(np.float16)
+    out = gpu_mmq(kai, [(qtype, w, to_dev(w))], to_dev(x))
+    cols = sample_cols(n, rng)
+    got = out[:, torch.from_numpy(cols).to(out.device)].cpu().numpy()
+    del out
+    ref = O.mmq_reference(qtype, w[cols], x, threads=16)
+    err = O.normwise_rel(got, ref)
+    print(f"  normwise rel err {err:.3e}")
+    assert err <= TOL_F32

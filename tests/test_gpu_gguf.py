@@ -81,8 +81,9 @@ def test_model_file_drives_the_fused_path(kai, tmp_path):
         print(f"gguf-loaded Q4_K m={m}", flush=True)
         x = to_dev(rng.standard_normal((m, k)).astype(np.float32)).to(torch.bfloat16)
         y = method.apply(layer, x)
-        ref = O.mul_mat(O.Q4_K, np.ascontiguousarray(w_host), k,
-                        O.prepare(x.view(torch.int16).cpu().numpy().view(np.uint16), dtype_code=1), m)
+        xb = x.view(torch.int16).cpu().numpy().view(np.uint16)
+        ref = O.mul_mat(O.Q4_K, np.ascontiguousarray(w_host), k, O.prepare(xb, dtype_code=1), m) if m <= 8 \
+            else O.mmq_reference(O.Q4_K, np.ascontiguousarray(w_host), xb, 1)
         assert O.normwise_rel(y.float().cpu().numpy(), ref) <= 2 * TOL_BF16
 
     a, b, s = 4, 8, 64
@@ -97,6 +98,7 @@ def test_model_file_drives_the_fused_path(kai, tmp_path):
         x = to_dev(rng.standard_normal((m, k)).astype(np.float32)).to(torch.bfloat16)
         y = method.apply(layer, x)
         xs = x[:, gather].contiguous()   # the stored-column order of the activation
-        ref = O.mul_mat(O.Q6_K, wb, k, O.prepare(xs.view(torch.int16).cpu().numpy().view(np.uint16),
-                                                dtype_code=1), m)
+        xb = xs.view(torch.int16).cpu().numpy().view(np.uint16)
+        ref = O.mul_mat(O.Q6_K, wb, k, O.prepare(xb, dtype_code=1), m) if m <= 8 \
+            else O.mmq_reference(O.Q6_K, wb, xb, 1)
         assert O.normwise_rel(y.float().cpu().numpy(), ref) <= 2 * TOL_BF16

@@ -69,9 +69,8 @@ def test_mul_mat_a8_against_oracle(kai, qtype, m, dtype):
     w = _weights(qtype, n, k, rng, "quantized")
     x = to_dev(rng.standard_normal((m, k)).astype(np.float32)).to(dtype)
     xh = x.cpu()
-    act = O.prepare(xh.view(torch.int16).numpy().view(np.uint16), dtype_code=1) if dtype == torch.bfloat16 \
-        else O.prepare(xh.numpy())
-    ref = O.mul_mat(qtype, w, k, act, m)
+    xb, code = (xh.view(torch.int16).numpy().view(np.uint16), 1) if dtype == torch.bfloat16 else (xh.numpy(), None)
+    ref = O.mul_mat(qtype, w, k, O.prepare(xb, dtype_code=code), m) if m <= 8 else O.mmq_reference(qtype, w, xb, code)
     op = ggml_mul_mat_vec_a8 if m <= 8 else ggml_mul_mat_a8
     y = op(to_dev(w), x, qtype, n)
     assert y.dtype == dtype and y.shape == (m, n)
@@ -93,7 +92,8 @@ def test_fused_mul_mat_gguf_dispatch(kai):
     for m in (1, 2, 7, 33):
         print(f"fused_mul_mat_gguf Q4_K m={m}", flush=True)
         xm = to_dev(rng.standard_normal((m, k)).astype(np.float16))
-        ref = O.mul_mat(O.Q4_K, w, k, O.prepare(xm.cpu().numpy()), m)
+        xn = xm.cpu().numpy()
+        ref = O.mul_mat(O.Q4_K, w, k, O.prepare(xn), m) if m <= 8 else O.mmq_reference(O.Q4_K, w, xn)
         y = fused_mul_mat_gguf(xm, to_dev(w), O.Q4_K)
         assert y.dtype == torch.float16
         assert O.normwise_rel(y.float().cpu().numpy(), ref) <= OUT_TOL[torch.float16]

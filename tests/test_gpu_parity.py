@@ -1,9 +1,12 @@
 """Parity of the gfx950 kernels with the CPU oracle, called through the C ABI.
 
-Bars: Q8_1 activation bytes bit-exact; GEMV/GEMM outputs within 1e-3 normwise
-max-rel (max|y - ref| / max|ref| per activation row) of the oracle's FP64 result
-for F32 output, and within 2^-8 for BF16 output (bf16 keeps 8 significant bits,
-so rounding alone reaches 2^-9 of max|y|).
+Bars: activation bytes bit-exact (the decode path's Q8_1 blocks, and the batched path's
+GGML MMQ planes read back from the scratch); GEMV/GEMM outputs within 1e-3 normwise
+max-rel (max|y - ref| / max|ref| per activation row) of the oracle's FP64 result for F32
+output, and within 2^-8 for BF16 output (bf16 keeps 8 significant bits, so rounding alone
+reaches 2^-9 of max|y|). Up to 8 rows the reference is the decode arithmetic
+(oracle_prepare + oracle_mul_mat); above 8 rows it is the batched path's
+(oracle_prepare_mmq + oracle_mul_mat_mmq, O.mmq_reference).
 """
 import ctypes
 
@@ -179,7 +182,7 @@ def test_two_pass_is_closer_to_float_activations(kai):
 
 # ----------------------------------------------------------------- batched group (kai_fused_mmq_run)
 
-def gpu_mmq(kai, mats, x_dev, bf16=False, stride=0):
+def gpu_mmq(kai, mats, x_dev, bf16=False, stride=0, return_scratch=False):
     m, k = x_dev.shape
     count = len(mats)
     types = (ctypes.c_int * count)(*[t for t, _, _ in mats])
@@ -196,7 +199,63 @@ def gpu_mmq(kai, mats, x_dev, bf16=False, stride=0):
                                out.data_ptr(), 1 if bf16 else 0, stride, scratch.data_ptr(), size, 0, _stream())
     assert st == 0, kai.current_direct_error()
     torch.cuda.synchronize()
+    return (out, scratch) if return_scratch else out
+
+
+def batched_ref(mats, x, dtype_code=None, threads=8):
+    """The batched path's result for a group: each matrix on its layout's plane."""
+    return np.concatenate([O.mmq_reference(t, w, x, dtype_code, threads) for t, w, *_ in mats], axis=1)
+
+
+def host_bits(x_dev):
+    """x as the oracle takes it: float32/float16 arrays, bf16 as uint16 bits (code 1)."""
+    if x_dev.dtype == torch.bfloat16:
+        return x_dev.view(torch.int16).cpu().numpy().view(np.uint16), 1
+    return x_dev.cpu().numpy(), None
+
+
+def plane_offsets(m, k, layouts):
+    """Scratch offsets of kai_fused_mmq_run: [inverse][plane D4][plane DS4][plane D2S6]..."""
+    a256 = lambda b: (b + 255) // 256 * 256
+    off = a256(4 * m)
+    plane = O.mmq_blocks128(k) * m * 144
+    out = {}
+    for l in (O.D4, O.DS4, O.D2S6):
+        if l in layouts:
+            out[l] = off
+            off += a256(plane)
     return out
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,k", [(9, 256), (17, 1056), (80, 5120), (130, 2080)])
+def test_mmq_planes_bit_exact(kai, dtype, m, k):
+    """The batched path's activation (row scale + GGML MMQ quantisation into D4, DS4 and
+    D2S6 planes, K padded to 512) read back from the scratch equals the oracle's bytes."""
+    print(f"mmq planes dtype={dtype} m={m} k={k}", flush=True)
+    rng = np.random.default_rng(m + k)
+    kq = k if k % 256 == 0 else None
+    types = [O.Q8_0, O.Q4_0] + ([O.Q2_K] if kq else [])
+    mats = []
+    for qtype in types:
+        w = O.random_blocks(qtype, 12, k, rng)
+        mats.append((qtype, w, to_dev(w)))
+    x = (rng.standard_normal((m, k)) * rng.uniform(1e-2, 1e2, (m, 1))).astype(np.float32)
+    x[0] = 0.0
+    x[1, :64] = 0.0
+    x[2, 5] = np.float32(np.finfo(np.float32).tiny) if dtype == torch.float32 else x[2, 5]
+    x_dev = to_dev(x).to(dtype)
+    out, scratch = gpu_mmq(kai, mats, x_dev, return_scratch=True)
+    xs, code = host_bits(x_dev)
+    layouts = {O.mmq_layout(t) for t in types}
+    offs = plane_offsets(m, k, layouts)
+    got = scratch.cpu().numpy()
+    for layout in layouts:
+        plane, inverse = O.prepare_mmq(xs, layout, code)
+        nbytes = plane.size
+        assert np.array_equal(got[offs[layout]:offs[layout] + nbytes], plane.reshape(-1)), O.LAYOUT_NAMES[layout]
+        assert np.array_equal(got[:4 * m].view(np.float32), inverse)
+    assert O.normwise_rel(out.cpu().numpy(), batched_ref(mats, xs, code)) <= TOL_F32
 
 
 @pytest.mark.parametrize("m", [9, 16, 17, 40, 80])
@@ -209,8 +268,7 @@ def test_mmq_group_parity(kai, m):
         w = O.random_blocks(qtype, n, k, rng)
         mats.append((qtype, w, to_dev(w)))
     x = rng.standard_normal((m, k)).astype(np.float16)
-    act = O.prepare(x)
-    ref = np.concatenate([O.mul_mat(t, w, k, act, m) for t, w, _ in mats], axis=1)
+    ref = batched_ref(mats, x)
     out = gpu_mmq(kai, mats, to_dev(x)).cpu().numpy()
     assert O.normwise_rel(out, ref) <= TOL_F32
     outb = gpu_mmq(kai, mats, to_dev(x), bf16=True, stride=ref.shape[1] + 8).float().cpu().numpy()
@@ -233,7 +291,7 @@ def test_mmq_each_type(kai, qtype, m, k, n):
     rng = np.random.default_rng(qtype * 1000 + m + k)
     w = O.random_blocks(qtype, n, k, rng)
     x = rng.standard_normal((m, k)).astype(np.float32)
-    ref = O.mul_mat(qtype, w, k, O.prepare(x), m)
+    ref = O.mmq_reference(qtype, w, x)
     out = gpu_mmq(kai, [(qtype, w, to_dev(w))], to_dev(x)).cpu().numpy()
     assert O.normwise_rel(out, ref) <= TOL_F32
 
@@ -269,26 +327,20 @@ def test_mmq_prefill_shape(kai, qtype):
     rng = np.random.default_rng(qtype + 5)
     w = O.random_blocks(qtype, n, k, rng)
     x_dev = to_dev(rng.standard_normal((m, k)).astype(np.float32)).to(torch.bfloat16)
-    act = O.prepare(x_dev.view(torch.int16).cpu().numpy().view(np.uint16), dtype_code=1)
-    ref = O.mul_mat(qtype, w, k, act, m, threads=16)
+    ref = O.mmq_reference(qtype, w, host_bits(x_dev)[0], 1, threads=16)
     out = gpu_mmq(kai, [(qtype, w, to_dev(w))], x_dev).cpu().numpy()
     assert O.normwise_rel(out, ref) <= TOL_F32
 
 
-# Formats on the fp16-MFMA prefill GEMM. The library routes a matrix there from 160 tiles of
-# 96 activation rows x 256 weight rows on (fewer go to the int8 kernel), so these shapes
-# are large enough in m * n; k stays small for the CPU oracle.
-MMF_TYPES = [O.Q4_K]
-
-
-@pytest.mark.parametrize("qtype", MMF_TYPES, ids=lambda t: O.NAMES[t])
+# Prefill-sized products: partial tiles in both dimensions (the last weight tile a 4-row
+# group, the last activation tile 40 rows), one to eight superblocks, wire blocks from random
+# bytes and from quantised N(0, 0.02) weights (whose min terms cancel: the product is only as
+# close to the reference as the fp16 roundings of the weight scales are repeated).
+@pytest.mark.parametrize("qtype", [O.Q4_K, O.Q2_K], ids=lambda t: O.NAMES[t])
 @pytest.mark.parametrize("weights", ["random", "quantized"])
 @pytest.mark.parametrize("m,n,k", [(1000, 4100, 256), (960, 4096, 1280), (1100, 3840, 2048)])
-def test_mmf_parity(kai, qtype, weights, m, n, k):
-    """fp16-MFMA GEMM: exact and partial tiles in both dimensions (the last weight tile
-    one 4-row group, the last activation tile 40 rows), one to eight superblocks, wire
-    blocks from random bytes and from quantised N(0, 0.02) weights."""
-    print(f"mmf type={qtype} {weights} m={m} n={n} k={k}", flush=True)
+def test_batched_prefill_tiles(kai, qtype, weights, m, n, k):
+    print(f"batched prefill tiles {O.NAMES[qtype]} {weights} m={m} n={n} k={k}", flush=True)
     rng = np.random.default_rng(qtype + m + n + k)
     if weights == "random":
         w = O.random_blocks(qtype, n, k, rng)
@@ -296,14 +348,14 @@ def test_mmf_parity(kai, qtype, weights, m, n, k):
         from kaillm_amd.formats import quantize
         w = quantize(rng.normal(0.0, 0.02, (n, k)).astype(np.float32), qtype)
     x = rng.standard_normal((m, k)).astype(np.float32)
-    ref = O.mul_mat(qtype, w, k, O.prepare(x), m, threads=16)
+    ref = O.mmq_reference(qtype, w, x, threads=16)
     out = gpu_mmq(kai, [(qtype, w, to_dev(w))], to_dev(x)).cpu().numpy()
     err = O.normwise_rel(out, ref)
     print(f"  normwise rel err {err:.3e}")
     assert err <= TOL_F32
 
 
-def test_mmf_heavy_tailed_activations_bf16_out_and_stride(kai):
+def test_batched_heavy_tailed_activations_bf16_out_and_stride(kai):
     """Activations spread over many binades (small-scale blocks beside large ones) and
     exact zeros; bf16 output into a wider matrix, the padding left untouched."""
     rng = np.random.default_rng(5)
@@ -312,8 +364,7 @@ def test_mmf_heavy_tailed_activations_bf16_out_and_stride(kai):
     x = (rng.standard_normal((m, k)) * np.exp(rng.normal(0.0, 2.0, (m, k)))).astype(np.float32)
     x[3] = 0.0
     x[7, :512] = 0.0
-    act = O.prepare(x)
-    ref = O.mul_mat(O.Q4_K, w, k, act, m, threads=16)
+    ref = O.mmq_reference(O.Q4_K, w, x, threads=16)
     out = gpu_mmq(kai, [(O.Q4_K, w, to_dev(w))], to_dev(x)).cpu().numpy()
     assert np.all(out[3] == 0.0)
     assert O.normwise_rel(out, ref) <= TOL_F32
@@ -322,74 +373,54 @@ def test_mmf_heavy_tailed_activations_bf16_out_and_stride(kai):
     assert np.isnan(outb[:, n:]).all()
 
 
-def test_mmf_group_with_int8_path(kai):
-    """A group where Q4_K matrices run on the fp16-MFMA GEMM (first and last) and the others
-    on the int8 kernel (one scratch, both preparations): Q6_K (format), a Q4_K after a column
-    offset of 2 mod 4 (unaligned output) and a narrow Q4_K (too few tiles, n = 2 mod 4)."""
+def test_batched_group_with_unaligned_columns(kai):
+    """One group, one scratch, three layouts: Q4_K matrices first and last, a Q6_K between
+    them, a Q4_K after a column offset of 2 mod 4 and a narrow Q4_K (n = 2 mod 4)."""
     rng = np.random.default_rng(11)
     m, k = 1000, 512
     mats = []
-    for qtype, n in ((O.Q4_K, 4096), (O.Q6_K, 130), (O.Q4_K, 4096), (O.Q4_K, 126), (O.Q4_K, 4096)):
+    for qtype, n in ((O.Q4_K, 4096), (O.Q6_K, 130), (O.Q4_K, 4096), (O.Q2_K, 126), (O.Q4_K, 4096)):
         w = O.random_blocks(qtype, n, k, rng)
         mats.append((qtype, w, to_dev(w)))
     x = rng.standard_normal((m, k)).astype(np.float16)
-    ref = np.concatenate([O.mul_mat(t, w, k, O.prepare(x), m, threads=16) for t, w, _ in mats], axis=1)
+    ref = batched_ref(mats, x, threads=16)
     out = gpu_mmq(kai, mats, to_dev(x)).cpu().numpy()
     assert O.normwise_rel(out, ref) <= TOL_F32
 
 
-PREFILL = [("C4 Q4_K gate/up", O.Q4_K, 34816, 5120, 512), ("C4 Q4_K down", O.Q4_K, 5120, 17408, 1024)]
-
-
-@pytest.mark.parametrize("name,qtype,n,k,m", PREFILL, ids=[p[0] for p in PREFILL])
-def test_prefill_configs(kai, name, qtype, n, k, m):
-    """BASELINE config 4 weights (bf16 activations, quantised N(0, 0.02)) at m = 512 and, for
-    the narrow down projection, m = 1024 (both on the fp16-MFMA GEMM)."""
-    print(f"prefill {name} m={m}", flush=True)
-    from kaillm_amd.formats import quantize
-    rng = np.random.default_rng(n + m)
-    w = quantize(rng.normal(0.0, 0.02, (n, k)).astype(np.float32), qtype)
-    x_dev = to_dev(rng.standard_normal((m, k)).astype(np.float32)).to(torch.bfloat16)
-    act = O.prepare(x_dev.view(torch.int16).cpu().numpy().view(np.uint16), dtype_code=1)
-    ref = O.mul_mat(qtype, w, k, act, m, threads=16)
-    out = gpu_mmq(kai, [(qtype, w, to_dev(w))], x_dev).cpu().numpy()
-    err = O.normwise_rel(out, ref)
-    print(f"  normwise rel err {err:.3e}")
-    assert err <= TOL_F32
-
-
-# Small-M GEMM on fp16 MFMA (9..16 rows through the batched entry): K split across the
-# waves of a workgroup (small n), partial row tiles, one and an odd number of superblocks.
+# Small batches (9..16 rows): K split across the waves of a workgroup (small n), partial
+# row tiles, one and an odd number of superblocks.
+@pytest.mark.parametrize("qtype", [O.Q4_K, O.Q6_K, O.Q2_K], ids=lambda t: O.NAMES[t])
 @pytest.mark.parametrize("weights", ["random", "quantized"])
 @pytest.mark.parametrize("m,n,k", [(9, 1000, 256), (12, 200, 1280), (16, 4100, 2304), (13, 64, 5120)])
-def test_mfv_parity(kai, weights, m, n, k):
-    print(f"mfv m={m} n={n} k={k} {weights}", flush=True)
+def test_batched_small_m(kai, qtype, weights, m, n, k):
+    print(f"batched small m {O.NAMES[qtype]} m={m} n={n} k={k} {weights}", flush=True)
     rng = np.random.default_rng(m * 7 + n + k)
     if weights == "random":
-        w = O.random_blocks(O.Q4_K, n, k, rng)
+        w = O.random_blocks(qtype, n, k, rng)
     else:
         from kaillm_amd.formats import quantize
-        w = quantize(rng.normal(0.0, 0.02, (n, k)).astype(np.float32), O.Q4_K)
+        w = quantize(rng.normal(0.0, 0.02, (n, k)).astype(np.float32), qtype)
     x = rng.standard_normal((m, k)).astype(np.float16)
-    ref = O.mul_mat(O.Q4_K, w, k, O.prepare(x), m, threads=16)
-    out = gpu_mmq(kai, [(O.Q4_K, w, to_dev(w))], to_dev(x)).cpu().numpy()
+    ref = O.mmq_reference(qtype, w, x, threads=16)
+    out = gpu_mmq(kai, [(qtype, w, to_dev(w))], to_dev(x)).cpu().numpy()
     err = O.normwise_rel(out, ref)
     print(f"  normwise rel err {err:.3e}")
     assert err <= TOL_F32
 
 
-def test_mfv_heavy_tailed_bf16_out_stride_and_group(kai):
-    """Heavy-tailed activations, BF16 output into a wider merged tile, and a group that
-    mixes the small-M GEMM (Q4_K) with the int8 kernel (Q6_K) behind one preparation."""
+def test_batched_heavy_tailed_bf16_out_stride_and_group(kai):
+    """Heavy-tailed activations, BF16 output into a wider merged tile, and a group of
+    Q4_K and Q6_K matrices behind one preparation."""
     m, k = 15, 1536
-    print(f"mfv group m={m} k={k}", flush=True)
+    print(f"batched group m={m} k={k}", flush=True)
     rng = np.random.default_rng(77)
     mats = []
     for qtype, n in ((O.Q4_K, 520), (O.Q6_K, 72), (O.Q4_K, 36)):
         w = O.random_blocks(qtype, n, k, rng)
         mats.append((qtype, w, to_dev(w)))
     x = (rng.standard_t(2.0, (m, k)) * 3.0).astype(np.float32)
-    ref = np.concatenate([O.mul_mat(t, w, k, O.prepare(x), m) for t, w, _ in mats], axis=1)
+    ref = batched_ref(mats, x)
     out = gpu_mmq(kai, mats, to_dev(x)).cpu().numpy()
     assert O.normwise_rel(out, ref) <= TOL_F32
     outb = gpu_mmq(kai, mats, to_dev(x), bf16=True, stride=ref.shape[1] + 4).float().cpu().numpy()
@@ -420,7 +451,7 @@ def test_full_size_configs(kai, name, qtype, n, k, m):
     w = O.random_blocks(qtype, n, k, rng)
     x = rng.standard_normal((m, k)).astype(np.float16)
     x_dev = to_dev(x)
-    ref = O.mul_mat(qtype, w, k, O.prepare(x), m, threads=16)
+    ref = O.mul_mat(qtype, w, k, O.prepare(x), m, threads=16) if m <= 8 else O.mmq_reference(qtype, w, x, threads=16)
     if m <= 8:
         out = gpu_mmvq(kai, qtype, to_dev(w), n, k, gpu_prepare(kai, x_dev), m)
     else:
@@ -445,8 +476,12 @@ def test_fused_projection_torch_ops(kai):
     for m in (1, 3, 8, 12, 64):
         x = rng.standard_normal((m, k)).astype(np.float32)
         x_dev = to_dev(x).to(torch.bfloat16)
-        act = O.prepare(x_dev.view(torch.int16).cpu().numpy().view(np.uint16), dtype_code=1)
-        ref = np.concatenate([O.mul_mat(t, w, k, act, m) for t, w in parts_np], axis=1)
+        xb = host_bits(x_dev)[0]
+        if m <= 8:
+            act = O.prepare(xb, dtype_code=1)
+            ref = np.concatenate([O.mul_mat(t, w, k, act, m) for t, w in parts_np], axis=1)
+        else:
+            ref = batched_ref(parts_np, xb, 1)
         bias = torch.randn(ref.shape[1], device=DEV, dtype=torch.bfloat16)
         y = method.apply(layer, x_dev.reshape(1, m, k), bias)
         assert y.shape == (1, m, ref.shape[1]) and y.dtype == torch.bfloat16

@@ -158,10 +158,9 @@ def test_apply_swiglu_small_and_large_batches(kai):
         y = method.apply_swiglu(layer, gu, act_fn)
         assert y.shape == (1, m, 256) and y.dtype == torch.bfloat16
         if m <= 8:  # the producer path
-            act = O.prepare_swiglu(host(gu.reshape(m, 2 * k)))
+            ref = O.mul_mat(O.Q4_K, parts_np[0][1], k, O.prepare_swiglu(host(gu.reshape(m, 2 * k))), m)
         else:       # act_fn, then the batched path
-            act = O.prepare(host(act_fn(gu).reshape(m, k)), dtype_code=1)
-        ref = O.mul_mat(O.Q4_K, parts_np[0][1], k, act, m)
+            ref = O.mmq_reference(O.Q4_K, parts_np[0][1], host(act_fn(gu).reshape(m, k)), 1)
         assert O.normwise_rel(y.float().reshape(m, -1).cpu().numpy(), ref) <= 2 * TOL_BF16
 
 
