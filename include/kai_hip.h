@@ -102,15 +102,21 @@ int kai_fused_mmvq(const void *weight, int type, int64_t n, int64_t k, int64_t m
                    int64_t stride_dst, uintptr_t stream);
 
 /* Scratch bytes kai_fused_mmq_run needs for `count` matrices (types[i], rows[i])
- * sharing k, at m > 8 activation rows. direct_f32 is accepted for signature
- * compatibility. Replaces kai_fused_mmq_workspace (current_ggml_direct.cu:1196-1205). */
+ * sharing k, at m > 8 activation rows: [inverse: m floats][one activation plane per
+ * layout the group reads, D4 then DS4 then D2S6], each region padded to 256 bytes; a plane
+ * is 128-value blocks of 144 bytes in [k/128][m] order with k padded to 512.
+ * direct_f32 is accepted for signature compatibility (outputs are always stored in
+ * place). Replaces kai_fused_mmq_workspace (current_ggml_direct.cu:1196-1205). */
 size_t kai_fused_mmq_workspace(int device, const int *types, const int64_t *rows, int count,
                                int64_t k, int64_t m, int direct_f32);
 
 /* Batched projection group for m > 8 rows (multi-sequence decode, spec-verify,
- * prefill): one activation preparation, then every matrix writes its column
- * slice of dst [m, sum rows] (row stride stride_dst, or sum rows when 0); F32 or
- * BF16. Replaces kai_fused_mmq_run (current_ggml_direct.cu:1207-1265). */
+ * prefill): one activation preparation (the power-of-two row normalisation, then GGML's
+ * MMQ quantisation of each layout the group reads: D4 for Q8_0/Q6_K/IQ3_S, DS4 for
+ * Q4_0/Q4_K, D2S6 for Q2_K), then every matrix writes its column slice of dst
+ * [m, sum rows] (row stride stride_dst, or sum rows when 0); F32 or BF16. k is a whole
+ * number of each type's blocks and a multiple of 4; the sum of rows is a multiple of 4.
+ * Replaces kai_fused_mmq_run (current_ggml_direct.cu:1207-1265). */
 int kai_fused_mmq_run(const void *const *weights, const int *types, const int64_t *rows, int count,
                       const void *x, int x_dtype, int64_t stride_x, int64_t k, int64_t m,
                       void *dst, int dst_bf16, int64_t stride_dst, void *scratch, size_t scratch_bytes,

@@ -251,8 +251,13 @@ extern "C" int kai_fused_mmq_run(const void *const *weights, const int *types, c
         int current = -1;
         if (hipGetDevice(&current) != hipSuccess) throw kai::Error("No HIP device");
         if (current != device && hipSetDevice(device) != hipSuccess) throw kai::Error("Invalid device index");
-        run_mmq_group(weights, types, rows, count, x, x_dtype, stride_x, k, m, dst, dst_bf16 != 0, ld,
-                      static_cast<char *>(scratch), plan, stream_of(stream));
+        try {
+            run_mmq_group(weights, types, rows, count, x, x_dtype, stride_x, k, m, dst, dst_bf16 != 0, ld,
+                          static_cast<char *>(scratch), plan, stream_of(stream));
+        } catch (...) {
+            if (current != device) (void)hipSetDevice(current);
+            throw;
+        }
         if (current != device) (void)hipSetDevice(current);
     });
 }

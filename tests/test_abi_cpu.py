@@ -102,7 +102,7 @@ def test_dequantize_rejects_bad_arguments_before_any_launch(kai):
 def test_mmq_workspace_rules(kai):
     types = (ctypes.c_int * 2)(12, 14)
     rows = (ctypes.c_int64 * 2)(34816, 5120)
-    assert kai.kai_fused_mmq_workspace(0, types, rows, 2, 5120, 16, 0) >= O.activation_bytes(16, 5120)
+    assert kai.kai_fused_mmq_workspace(0, types, rows, 2, 5120, 16, 0) > 0
     assert kai.kai_fused_mmq_workspace(0, types, rows, 2, 5120, 8, 0) == 0          # needs m > 8
     assert b"more than 8" in kai.current_direct_error()
     assert kai.kai_fused_mmq_workspace(0, types, rows, 0, 5120, 16, 0) == 0         # empty group
@@ -113,6 +113,22 @@ def test_mmq_workspace_rules(kai):
     assert kai.kai_fused_mmq_run(ptrs, types, rows, 2, ctypes.c_void_p(16), 2, 5120, 5120, 16,
                                  ctypes.c_void_p(16), 0, 0, ctypes.c_void_p(16), 10, 0, 0) == -1
     assert b"scratch" in kai.current_direct_error()
+
+
+def _plane_bytes(m, k):
+    return (k + 511) // 512 * 4 * m * 144
+
+
+def test_mmq_workspace_is_inverse_then_one_plane_per_layout(kai):
+    """[inverse m f32][D4][DS4][D2S6], each 256-aligned, a plane only for a layout the group
+    reads (Q8_0/Q6_K/IQ3_S: D4; Q4_0/Q4_K: DS4; Q2_K: D2S6)."""
+    a256 = lambda b: (b + 255) // 256 * 256
+    for tl, m, k in (((12,), 16, 5120), ((12, 14), 80, 17408), ((10, 21, 2), 33, 1024), ((8,), 9, 1056)):
+        types = (ctypes.c_int * len(tl))(*tl)
+        rows = (ctypes.c_int64 * len(tl))(*([64] * len(tl)))
+        layouts = {O.mmq_layout(t) for t in tl}
+        want = a256(4 * m) + len(layouts) * a256(_plane_bytes(m, k))
+        assert kai.kai_fused_mmq_workspace(0, types, rows, len(tl), k, m, 1) == want
 
 
 @pytest.mark.parametrize("qtype", O.WEIGHT_TYPES, ids=lambda t: O.NAMES[t])
