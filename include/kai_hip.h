@@ -122,6 +122,23 @@ int kai_fused_mmq_run(const void *const *weights, const int *types, const int64_
                       void *dst, int dst_bf16, int64_t stride_dst, void *scratch, size_t scratch_bytes,
                       int device, uintptr_t stream);
 
+/* Largest scratch kai_fused_mmq_run_noalloc can use on one device (16 MiB), and the
+ * function that reports it. */
+#define KAI_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+size_t kai_fused_mmq_noalloc_capacity(void);
+
+/* kai_fused_mmq_run without the scratch arguments: the same arithmetic and kernels, with
+ * the scratch in a device array the library holds per GPU (KAI_NOALLOC_SCRATCH_BYTES, kept
+ * until the process ends). It allocates nothing, so callers that cannot allocate (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc) can use it.
+ * Returns -1 with a message when kai_fused_mmq_workspace(...) for the call exceeds the
+ * capacity. Every call on one GPU uses that GPU's array: calls that overlap on one GPU
+ * (two streams, or two host threads) race and must be ordered by the caller. No
+ * counterpart in the reference. */
+int kai_fused_mmq_run_noalloc(const void *const *weights, const int *types, const int64_t *rows, int count,
+                              const void *x, int x_dtype, int64_t stride_x, int64_t k, int64_t m,
+                              void *dst, int dst_bf16, int64_t stride_dst, int device, uintptr_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -4,6 +4,7 @@
 // launch going to the gfx950 kernels of this library.
 #include <algorithm>
 #include <climits>
+#include <mutex>
 #include <string>
 
 #include "../../include/kai_hip.h"
@@ -254,6 +255,68 @@ extern "C" int kai_fused_mmq_run(const void *const *weights, const int *types, c
         try {
             run_mmq_group(weights, types, rows, count, x, x_dtype, stride_x, k, m, dst, dst_bf16 != 0, ld,
                           static_cast<char *>(scratch), plan, stream_of(stream));
+        } catch (...) {
+            if (current != device) (void)hipSetDevice(current);
+            throw;
+        }
+        if (current != device) (void)hipSetDevice(current);
+    });
+}
+
+// ---------------------------------------------------------------- allocation-free batched entry
+// Scratch of kai_fused_mmq_run_noalloc: one array per GPU, in the code object. Host code
+// never passes this name to a kernel or a copy: its device address on each GPU comes from
+// hipGetSymbolAddress (noalloc_scratch_on below). Nothing in it needs clearing between
+// calls: the preparation writes every byte the GEMM reads.
+static __device__ __align__(256) uint8_t noalloc_scratch[KAI_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+
+// Device address of the array on `device` (current), looked up once per device.
+char *noalloc_scratch_on(int device) {
+    static std::mutex mutex;
+    static char *address[NOALLOC_MAX_DEVICES] = {};
+    if (device < 0 || device >= NOALLOC_MAX_DEVICES) throw kai::Error("Invalid device index");
+    std::lock_guard<std::mutex> lock(mutex);
+    if (!address[device]) {
+        void *ptr = nullptr;
+        const hipError_t status = hipGetSymbolAddress(&ptr, HIP_SYMBOL(noalloc_scratch));
+        if (status != hipSuccess || !ptr)
+            throw kai::Error(std::string("Cannot find the allocation-free scratch on this device: ") +
+                             hipGetErrorString(status));
+        address[device] = static_cast<char *>(ptr);
+    }
+    return address[device];
+}
+
+}  // namespace
+
+extern "C" size_t kai_fused_mmq_noalloc_capacity(void) { return KAI_NOALLOC_SCRATCH_BYTES; }
+
+extern "C" int kai_fused_mmq_run_noalloc(const void *const *weights, const int *types, const int64_t *rows,
+                                         int count, const void *x, int x_dtype, int64_t stride_x, int64_t k,
+                                         int64_t m, void *dst, int dst_bf16, int64_t stride_dst, int device,
+                                         uintptr_t stream) {
+    return entry([&] {
+        const Group g = validate_group(types, rows, count, k, m);
+        const MmqScratch plan = mmq_scratch(types, count, k, m);
+        if (plan.total > KAI_NOALLOC_SCRATCH_BYTES)
+            throw kai::Error("kai_fused_mmq_run_noalloc: this call needs " + std::to_string(plan.total) +
+                             " scratch bytes, above its 16 MiB capacity; use kai_fused_mmq_run");
+        if (!weights || !x || !dst || k % 4 || stride_x < k || device < 0)
+            throw kai::Error("Invalid fused MMQ pointers or strides");
+        for (int i = 0; i < count; ++i)
+            if (!weights[i]) throw kai::Error("Null packed matrix");
+        const int64_t ld = stride_dst ? stride_dst : g.total_rows;
+        if (ld < g.total_rows) throw kai::Error("Fused MMQ output stride is smaller than the output width");
+        int current = -1;
+        if (hipGetDevice(&current) != hipSuccess) throw kai::Error("No HIP device");
+        if (current != device && hipSetDevice(device) != hipSuccess) throw kai::Error("Invalid device index");
+        try {
+            run_mmq_group(weights, types, rows, count, x, x_dtype, stride_x, k, m, dst, dst_bf16 != 0, ld,
+                          noalloc_scratch_on(device), plan, stream_of(stream));
         } catch (...) {
             if (current != device) (void)hipSetDevice(current);
             throw;

@@ -47,6 +47,11 @@ def _load(path: str):
     lib.kai_fused_mmq_run.argtypes = [arr(ptr), arr(c_int), arr(i64), c_int, ptr, c_int, i64, i64, i64, ptr,
                                       c_int, i64, ptr, ctypes.c_size_t, c_int, u64]
     lib.kai_fused_mmq_run.restype = c_int
+    lib.kai_fused_mmq_noalloc_capacity.argtypes = []
+    lib.kai_fused_mmq_noalloc_capacity.restype = ctypes.c_size_t
+    lib.kai_fused_mmq_run_noalloc.argtypes = [arr(ptr), arr(c_int), arr(i64), c_int, ptr, c_int, i64, i64, i64, ptr,
+                                              c_int, i64, c_int, u64]
+    lib.kai_fused_mmq_run_noalloc.restype = c_int
     lib.kai_upload_rows.argtypes = [ctypes.c_char_p, i64, i64, i64, ptr, i64, i64, ptr, ptr, u64]
     lib.kai_upload_rows.restype = c_int
     lib.kai_dequantize.argtypes = [ptr, c_int, i64, i64, ptr, c_int, u64]

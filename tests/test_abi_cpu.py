@@ -131,6 +131,20 @@ def test_mmq_workspace_is_inverse_then_one_plane_per_layout(kai):
         assert kai.kai_fused_mmq_workspace(0, types, rows, len(tl), k, m, 1) == want
 
 
+def test_noalloc_capacity_and_oversized_call(kai):
+    assert kai.kai_fused_mmq_noalloc_capacity() == 16 << 20
+    types = (ctypes.c_int * 1)(14)
+    rows = (ctypes.c_int64 * 1)(5120)
+    ptrs = (ctypes.c_void_p * 1)(16)
+    # M = 2048 at K = 17408 needs 40 MiB of planes: refused before any device work
+    assert kai.kai_fused_mmq_run_noalloc(ptrs, types, rows, 1, ctypes.c_void_p(16), 2, 17408, 17408, 2048,
+                                         ctypes.c_void_p(16), 0, 0, 0, 0) == -1
+    assert b"16 MiB" in kai.current_direct_error()
+    assert kai.kai_fused_mmq_run_noalloc(ptrs, types, rows, 1, ctypes.c_void_p(16), 2, 17408, 17408, 8,
+                                         ctypes.c_void_p(16), 0, 0, 0, 0) == -1   # m <= 8
+    assert b"more than 8" in kai.current_direct_error()
+
+
 @pytest.mark.parametrize("qtype", O.WEIGHT_TYPES, ids=lambda t: O.NAMES[t])
 def test_quantizer_round_trip(qtype):
     """The host quantizer writes valid blocks whose oracle dequantization tracks the floats."""
