@@ -208,59 +208,68 @@ class GGUFReader:
         raise KeyError(name)
 
 
-def permute_stored(data: torch.Tensor, qtype: int, rows: torch.Tensor | None, columns: torch.Tensor | None):
-    """Row/column permutations of a stored matrix (yaqa_linear.py:102-127 of the reference).
+def inverse_permutation(columns: torch.Tensor) -> torch.Tensor:
+    """g with g[columns[i]] = i: the activation gather that matches a weight whose columns
+    were permuted by ``columns`` (x_stored = x.index_select(-1, g))."""
+    g = torch.empty_like(columns)
+    g.scatter_(0, columns, torch.arange(columns.numel(), dtype=columns.dtype, device=columns.device))
+    return g
 
-    Returns (data, gather). A column permutation that moves whole GGML blocks is applied to
-    the stored bytes; otherwise the stored columns are kept and ``gather`` (the inverse
-    permutation, x_stored = x.index_select(-1, gather)) permutes the activation.
-    """
+
+def block_order(columns: torch.Tensor, block: int) -> torch.Tensor | None:
+    """When ``columns`` only moves whole ``block``-value blocks (every run of ``block``
+    consecutive entries is one source block, in order), the source block of each stored
+    block; else None."""
+    n = columns.numel()
+    if n == 0 or n % block:
+        return None
+    sources = torch.div(columns[::block], block, rounding_mode="floor")
+    rebuilt = (sources[:, None] * block + torch.arange(block, dtype=columns.dtype, device=columns.device)).reshape(-1)
+    return sources.to(torch.long) if torch.equal(rebuilt, columns) else None
+
+
+def permute_stored(data: torch.Tensor, qtype: int, rows: torch.Tensor | None, columns: torch.Tensor | None):
+    """A stored matrix under the loader's row and column permutations
+    (the reference's _permute_stored, yaqa_linear.py:102-127): returns (data, gather).
+
+    Rows are reordered in place. A column permutation of a dense matrix is applied to it; on
+    wire bytes it is applied only when it moves whole GGML blocks (the blocks are reordered);
+    otherwise the bytes keep their order and ``gather`` reorders the activation instead."""
     if rows is not None:
         data = data[rows]
     if columns is None:
         return data, None
     if data.dtype != torch.uint8:
         return data[:, columns].contiguous(), None
-    order = block_order(columns, GGML_QUANT_SIZES[qtype][0])
-    if order is not None:
-        bb = GGML_QUANT_SIZES[qtype][1]
-        stored = data.reshape(data.shape[0], -1, bb)
-        return stored[:, order.to(data.device)].reshape(data.shape[0], -1).contiguous(), None
-    gather = torch.empty_like(columns)
-    gather[columns] = torch.arange(columns.numel(), dtype=columns.dtype, device=columns.device)
-    return data, gather
-
-
-def block_order(columns: torch.Tensor, block: int) -> torch.Tensor | None:
-    """Source block of each stored block when ``columns`` moves whole ``block``-value blocks."""
-    if columns.numel() % block:
-        return None
-    blocks = columns.reshape(-1, block)
-    starts = blocks[:, :1]
-    ramp = torch.arange(block, dtype=columns.dtype, device=columns.device).expand_as(blocks)
-    if not bool((starts % block == 0).all()) or not torch.equal(blocks - starts, ramp):
-        return None
-    return (starts[:, 0] // block).to(torch.long)
+    qk, bb = GGML_QUANT_SIZES[qtype]
+    order = block_order(columns, qk)
+    if order is None:
+        return data, inverse_permutation(columns)
+    blocks = data.reshape(data.shape[0], -1, bb).index_select(1, order.to(data.device))
+    return blocks.reshape(data.shape[0], -1).contiguous(), None
 
 
 def transpose_view(gather: torch.Tensor):
-    """(a, b, s) when gather == arange(n).view(a, b, s).transpose(0, 1).flatten(), else None
-    (yaqa_linear.py:130-148 of the reference): the input-view path of the fused producers."""
-    n = gather.numel()
-    values = gather.tolist()
-    if not values or values[0] != 0:
+    """(a, b, s) when the gather reads x's columns as [a][b][s] in the order [b][a][s], i.e.
+    gather[c] = ((c // s) % a) * b * s + (c // (a * s)) * s + c % s for every column c; else
+    None (the reference's _transpose_view, yaqa_linear.py:130-148). Such a gather is the
+    fused view producer's input (kai_fused_prepare_view)."""
+    g = gather.detach().to("cpu", torch.int64)
+    n = g.numel()
+    if n < 2 or int(g[0]) != 0:
         return None
-    s = 1
-    while s < n and values[s] == s:
-        s += 1
-    if s == n or n % s or values[s] % s:
+    # s: the length of the leading run 0, 1, 2, ... (a segment is copied whole)
+    steps = torch.nonzero(g[1:] - g[:-1] != 1)
+    if steps.numel() == 0:
         return None
-    b = values[s] // s
-    if b <= 1 or n % (b * s):
+    s = int(steps[0]) + 1
+    b = int(g[s]) // s
+    if n % s or int(g[s]) % s or b < 2 or n % (b * s):
         return None
     a = n // (b * s)
-    expected = torch.arange(n, dtype=gather.dtype, device=gather.device).view(a, b, s).transpose(0, 1)
-    return (a, b, s) if torch.equal(gather, expected.reshape(-1)) else None
+    c = torch.arange(n)
+    expect = ((c // s) % a) * (b * s) + (c // (a * s)) * s + c % s
+    return (a, b, s) if torch.equal(g, expect) else None
 
 
 def upload(reader: GGUFReader, tensor: ReaderTensor, device, rows: torch.Tensor | None = None,
@@ -305,9 +314,7 @@ def load_packed(reader: GGUFReader, name: str, dtype: torch.dtype, device,
     if column_permutation is not None:
         blocks = block_order(column_permutation.cpu(), qk)
         if blocks is None:
-            gather = torch.empty_like(column_permutation)
-            gather[column_permutation] = torch.arange(column_permutation.numel(), dtype=column_permutation.dtype,
-                                                      device=column_permutation.device)
+            gather = inverse_permutation(column_permutation)
     data = upload(reader, t, device, row_permutation, blocks)
     layer = PackedGGUFLinear(data, t.tensor_type, dtype)
     view = transpose_view(gather) if gather is not None else None
