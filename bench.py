@@ -1,21 +1,25 @@
 #!/usr/bin/env python3
 """Benchmark of the GGUF dequant-fused quantized linear on one MI355X.
 
-Workload ("C3"): Qwen-27B-like UD-Q4_K_XL mix, decode GEMV
-at batch 1, 2, 8 and 16 — Q4_K gate/up 34816x5120 and qkv 7168x5120, Q6_K down
-5120x17408 and o_proj 5120x6144, weights quantized from seeded N(0, 0.02),
-activations fp16 N(0, 1). One step = for each batch size, each projection's Q8_1
-activation preparation and its GEMV (rows <= 8: kai_fused_mmvq, 16:
-kai_fused_mmq_run), i.e. 16 projections. value = weight bytes streamed per step /
-step time (GB/s); inputs are resident in HBM.
+Headline workload ("C3"): Qwen-27B-like UD-Q4_K_XL mix at batch
+1, 2, 8 and 16 — Q4_K gate/up 34816x5120 and qkv 7168x5120, Q6_K down 5120x17408 and
+o_proj 5120x6144, weights quantized from seeded N(0, 0.02), activations fp16 N(0, 1). One
+step = for each batch size, each projection's activation preparation and its product
+(rows <= 8: kai_fused_prepare + kai_fused_mmvq; 16: kai_fused_mmq_run), 16 projections.
+value = weight bytes streamed per step / step time (GB/s); inputs are resident in HBM.
 
-Measurement: every step is a replay of a captured HIP graph; 3 copies of the
-weights (660 MB) rotate so the 256 MB Infinity Cache never holds the working set.
-The roofline object covers the dominant kernel, the Q4_K gate/up GEMV (100 MB of
-wire bytes per launch), timed by HIP events around replays of a graph of those
-launches alone (8 rounds of the 3 copies per graph). The prefill leg (configs[3],
-M=2048) reports TOPS. The CPU baseline times the oracle (the C restatement of the
-reference arithmetic) on a bounded sample on the host cores.
+Every timing is a replay of a captured HIP graph, HIP events on the replay stream, with
+rotating weight copies totalling >= 600 MB so the 256 MB Infinity Cache never holds the
+working set.
+
+* ``roofline``: the Q4_K gate/up decode kernel at batch 1, 2 and 8 (the GEMV, or the paired
+  int8 tile above the GEMV's row limit), kernel only: the activation is prepared once
+  outside the graph; 100 270 080 weight bytes per launch over the mean launch time.
+* ``legs``: every BASELINE config as whole calls (preparation included, as a caller sees
+  them): C1, C2 and C5 decode, C3 per matrix and batch, C4 spec-verify (M=80, GB/s) and
+  prefill (M=512, 2048, TOPS), C5 batch 16 and prefill. Each leg names its kernel.
+* ``cpu_baseline``: the oracle (the C restatement of the reference arithmetic) on a bounded
+  sample, on the host cores, with the CPU model and thread count.
 """
 import argparse
 import ctypes
@@ -32,8 +36,27 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
-COPIES = 3
-ROUNDS = 8  # rounds of the copies per timed graph, so graph-launch overhead is amortised
+ROTATION_BYTES = 600e6   # weight copies per matrix: at least this many bytes in rotation
+MIN_COPIES = 3
+
+# BASELINE.json configs as (config, matrix, type, n, k, batches)
+Q4_0, Q8_0, Q2_K, Q4_K, Q6_K, IQ3_S = 2, 8, 10, 12, 14, 21
+C3 = [("gate_up", Q4_K, 34816, 5120), ("qkv", Q4_K, 7168, 5120), ("down", Q6_K, 5120, 17408),
+      ("o_proj", Q6_K, 5120, 6144)]
+LEGS = [
+    ("C1", "plumbing", Q8_0, 2048, 2048, (1,)),
+    ("C2", "gate_up", Q4_0, 16384, 2048, (1, 2, 4, 8)),
+    ("C2", "down", Q4_0, 2048, 8192, (1, 2, 4, 8)),
+    ("C2", "qkv", Q4_0, 3072, 2048, (1, 2, 4, 8)),
+    ("C4", "gate_up", Q4_K, 34816, 5120, (80, 512, 2048)),
+    ("C4", "down", Q4_K, 5120, 17408, (80, 512, 2048)),
+    ("C5", "gate_up Q2_K", Q2_K, 34816, 5120, (1, 16, 2048)),
+    ("C5", "down Q2_K", Q2_K, 5120, 17408, (1, 16, 2048)),
+    ("C5", "gate_up IQ3_S", IQ3_S, 34816, 5120, (1, 16, 2048)),
+    ("C5", "down IQ3_S", IQ3_S, 5120, 17408, (1, 16, 2048)),
+]
+NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q2_K: "Q2_K", Q4_K: "Q4_K", Q6_K: "Q6_K", IQ3_S: "IQ3_S"}
+GEMV_MAX_ROWS = {Q4_0: 8, Q8_0: 8, Q4_K: 4, Q6_K: 4, IQ3_S: 4, Q2_K: 3}  # kai_launch.h gemv_max_rows
 
 
 def parse():
@@ -42,13 +65,115 @@ def parse():
     p.add_argument("--steps", type=int, default=60)
     p.add_argument("--warmup", type=int, default=6)
     p.add_argument("--batches", default="1,2,8,16")
+    p.add_argument("--legs", default="all", help="'all', 'none', or a comma list of C1,C2,C3,C4,C5")
+    p.add_argument("--reps", type=int, default=8, help="graph replays per leg")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    p.add_argument("--no-prefill", action="store_true", help="skip the prefill leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--kernel-sample", action="store_true",
                    help="counter-collection run: a 256 MiB device copy (calibration) and the dominant "
                         "GEMV on each weight copy, eager launches only")
     return p.parse_args()
+
+
+def kernel_name(qtype, m):
+    if m > 8:
+        return "int8 MMQ (kai_fused_mmq_run: GGML MMQ planes + mmq_kernel)"
+    if m <= GEMV_MAX_ROWS[qtype]:
+        return "v_dot4 GEMV (mmvq_kernel)"
+    return "paired int8 MMQ tile (mmq_kernel, PAIR)"
+
+
+class Runner:
+    """Weights (rotating copies), inputs, outputs and scratch of the projections benched."""
+
+    def __init__(self, lib, dev, torch, max_m):
+        self.lib, self.dev, self.torch = lib, dev, torch
+        self.weights, self.groups, self.ws = {}, {}, {}
+        self.max_m = max_m
+        self.stream = torch.cuda.Stream(device=dev)
+        self.rng = np.random.default_rng(2)
+        self.x, self.out, self.act = {}, {}, {}
+
+    def add(self, key, qtype, n, k, seed, max_m):
+        from kaillm_amd.formats import quantize, weight_bytes
+        torch = self.torch
+        if key in self.weights:
+            return
+        g = torch.Generator(device=self.dev).manual_seed(seed)
+        w32 = torch.randn((n, k), generator=g, device=self.dev, dtype=torch.float32).mul_(0.02).cpu().numpy()
+        packed = torch.from_numpy(quantize(w32, qtype)).to(self.dev)
+        del w32
+        copies = max(MIN_COPIES, int(np.ceil(ROTATION_BYTES / weight_bytes(qtype, n, k))))
+        self.weights[key] = [packed] + [packed.clone() for _ in range(copies - 1)]
+        self.groups[key] = [((ctypes.c_void_p * 1)(w.data_ptr()), (ctypes.c_int * 1)(qtype), (ctypes.c_int64 * 1)(n))
+                            for w in self.weights[key]]
+        if k not in self.x or self.x[k].shape[0] < max_m:
+            self.x[k] = torch.from_numpy(self.rng.standard_normal((max_m, k)).astype(np.float16)).to(self.dev)
+        if n not in self.out or self.out[n].numel() < max_m * n:
+            self.out[n] = torch.empty(max_m * n, dtype=torch.float32, device=self.dev)
+        if k not in self.act or self.act[k].numel() < self.lib.kai_fused_activation_bytes(8, k, 0):
+            self.act[k] = torch.empty(self.lib.kai_fused_activation_bytes(8, k, 0), dtype=torch.uint8,
+                                      device=self.dev)
+        if max_m > 8:
+            size = self.lib.kai_fused_mmq_workspace(0, self.groups[key][0][1], self.groups[key][0][2], 1, k, max_m, 1)
+            if size == 0:
+                raise RuntimeError(self.lib.current_direct_error().decode())
+            self.ws[key] = torch.empty(size, dtype=torch.uint8, device=self.dev)
+
+    def call(self, key, qtype, n, k, m, copy, s, prepare=True):
+        """One projection: preparation + product (decode), or one batched call."""
+        from kaillm_amd import native
+        lib, x = self.lib, self.x[k][:m]
+        if m <= 8:
+            if prepare:
+                native.check(lib, lib.kai_fused_prepare(x.data_ptr(), 2, m, k, k, self.act[k].data_ptr(), 0, s))
+            native.check(lib, lib.kai_fused_mmvq(self.weights[key][copy].data_ptr(), qtype, n, k, m,
+                                                 self.act[k].data_ptr(), 0, self.out[n].data_ptr(), 0, n, s))
+        else:
+            ptrs, types, rows = self.groups[key][copy]
+            ws = self.ws[key]
+            native.check(lib, lib.kai_fused_mmq_run(ptrs, types, rows, 1, x.data_ptr(), 2, k, k, m,
+                                                    self.out[n].data_ptr(), 0, 0, ws.data_ptr(), ws.numel(), 0, s))
+
+    def capture(self, fn):
+        torch = self.torch
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(self.stream):
+            fn()  # once outside capture (code-object loading, LDS attributes)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=self.stream):
+                fn()
+        return g
+
+    def timed(self, graphs, reps, warmup):
+        """ms per replay (HIP events on the replay stream)."""
+        torch = self.torch
+        with torch.cuda.stream(self.stream):
+            for i in range(warmup):
+                graphs[i % len(graphs)].replay()
+            torch.cuda.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(self.stream)
+            for i in range(reps):
+                graphs[i % len(graphs)].replay()
+            end.record(self.stream)
+            torch.cuda.synchronize()
+        return start.elapsed_time(end) / reps
+
+    def per_launch_us(self, key, qtype, n, k, m, reps, warmup, prepare=True, budget_ms=40.0):
+        """Mean time of one call, from a graph of calls over every weight copy (rounds of the
+        copies until the graph holds about budget_ms of work)."""
+        copies = len(self.weights[key])
+        one = self.timed([self.capture(lambda: self.call(key, qtype, n, k, m, 0, self.stream.cuda_stream,
+                                                         prepare))], 3, 1)
+        rounds = max(1, min(int(budget_ms / max(one * copies, 1e-3)), 2000 // copies))
+        seq = [c for _ in range(rounds) for c in range(copies)]
+
+        def fn():
+            s = self.torch.cuda.current_stream().cuda_stream
+            for c in seq:
+                self.call(key, qtype, n, k, m, c, s, prepare)
+        return self.timed([self.capture(fn)], reps, warmup) / len(seq) * 1e3
 
 
 def main():
@@ -60,7 +185,7 @@ def main():
     import torch
 
     from kaillm_amd import native
-    from kaillm_amd.formats import Q4_K, Q6_K, quantize, weight_bytes
+    from kaillm_amd.formats import weight_bytes
 
     lib = native.library()
     dev = torch.device("cuda:0")
@@ -69,158 +194,91 @@ def main():
     if args.kernel_sample:
         kernel_sample(lib, dev, batches)
         return
+    chosen = set(("C1,C2,C3,C4,C5" if args.legs == "all" else "" if args.legs == "none" else args.legs).split(","))
 
-    mats = [  # name, type, n, k
-        ("gate_up", Q4_K, 34816, 5120),
-        ("qkv", Q4_K, 7168, 5120),
-        ("down", Q6_K, 5120, 17408),
-        ("o_proj", Q6_K, 5120, 6144),
-    ]
-    rng = np.random.default_rng(2)
     t0 = time.time()
-    weights = {}
-    for i, (name, qtype, n, k) in enumerate(mats):
-        g = torch.Generator(device=dev).manual_seed(1000 + i)
-        w32 = torch.randn((n, k), generator=g, device=dev, dtype=torch.float32).mul_(0.02).cpu().numpy()
-        packed = torch.from_numpy(quantize(w32, qtype)).to(dev)
-        del w32
-        weights[name] = [packed] + [packed.clone() for _ in range(COPIES - 1)]
-    print(f"[bench] weights quantized and uploaded in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    r = Runner(lib, dev, torch, max(batches))
+    for i, (name, qtype, n, k) in enumerate(C3):
+        r.add(("C3", name), qtype, n, k, 1000 + i, max(batches))
+    print(f"[bench] C3 weights quantized and uploaded in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
 
-    stream = torch.cuda.Stream(device=dev)
-    max_m = max(batches)
-    xs = {name: torch.from_numpy(rng.standard_normal((max_m, k)).astype(np.float16)).to(dev)
-          for name, _, _, k in mats}
-    outs = {name: torch.empty((max_m, n), dtype=torch.float32, device=dev) for name, _, n, _ in mats}
-    acts = {name: torch.empty(lib.kai_fused_activation_bytes(max_m, k, 0), dtype=torch.uint8, device=dev)
-            for name, _, _, k in mats}
-    groups = {}
-    for name, qtype, n, k in mats:
-        for c in range(COPIES):
-            groups[(name, c)] = ((ctypes.c_void_p * 1)(weights[name][c].data_ptr()),
-                                 (ctypes.c_int * 1)(qtype), (ctypes.c_int64 * 1)(n))
-    # scratch of the batched entry at the largest batch (its size query, as the reference's
-    # callers do)
-    mmq_ws = {}
-    for name, qtype, n, k in mats:
-        ptrs, types, rows = groups[(name, 0)]
-        size = lib.kai_fused_mmq_workspace(0, types, rows, 1, k, max_m, 1) if max_m > 8 else 0
-        mmq_ws[name] = torch.empty(max(size, 1), dtype=torch.uint8, device=dev)
-
-    def projection(name, qtype, n, k, m, copy, s):
-        x = xs[name][:m]
-        if m <= 8:
-            native.check(lib, lib.kai_fused_prepare(x.data_ptr(), 2, m, k, k, acts[name].data_ptr(), 0, s))
-            native.check(lib, lib.kai_fused_mmvq(weights[name][copy].data_ptr(), qtype, n, k, m,
-                                                 acts[name].data_ptr(), 0, outs[name].data_ptr(), 0, n, s))
-        else:
-            ptrs, types, rows = groups[(name, copy)]
-            native.check(lib, lib.kai_fused_mmq_run(ptrs, types, rows, 1, x.data_ptr(), 2, k, k, m,
-                                                    outs[name].data_ptr(), 0, 0, mmq_ws[name].data_ptr(),
-                                                    mmq_ws[name].numel(), 0, s))
-
-    def capture(fn):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(stream):
-            fn()  # warm once outside capture (module/code-object loading)
-            torch.cuda.synchronize()
-            with torch.cuda.graph(g, stream=stream):
-                fn()
-        return g
-
-    def step_fn(copy_base):
+    # ---- headline: the C3 decode step
+    def step_fn(base):
         def fn():
             s = torch.cuda.current_stream().cuda_stream
             for bi, m in enumerate(batches):
-                for name, qtype, n, k in mats:
-                    projection(name, qtype, n, k, m, (copy_base + bi) % COPIES, s)
+                for name, qtype, n, k in C3:
+                    key = ("C3", name)
+                    r.call(key, qtype, n, k, m, (base + bi) % len(r.weights[key]), s)
         return fn
+    step_graphs = [r.capture(step_fn(c)) for c in range(MIN_COPIES)]
+    step_bytes = sum(weight_bytes(q, n, k) for _, q, n, k in C3) * len(batches)
+    ms_step = r.timed(step_graphs, args.steps, args.warmup)
+    print(f"[bench] step {ms_step * 1e3:.1f} us for {step_bytes / 1e6:.1f} MB of weights", file=sys.stderr,
+          flush=True)
 
-    step_graphs = [capture(step_fn(c)) for c in range(COPIES)]
-    step_bytes = sum(weight_bytes(q, n, k) for _, q, n, k in mats) * len(batches)
-
-    def timed(graphs, reps):
-        for i in range(args.warmup):
-            graphs[i % len(graphs)].replay()
+    # ---- roofline: Q4_K gate/up decode kernel alone (activation prepared outside the graph)
+    name, qtype, n, k = C3[0]
+    key = ("C3", name)
+    decode = [m for m in batches if m <= 8]
+    kernel_us = {}
+    for m in decode:
+        x = r.x[k][:m]
+        native.check(lib, lib.kai_fused_prepare(x.data_ptr(), 2, m, k, k, r.act[k].data_ptr(), 0,
+                                                torch.cuda.current_stream().cuda_stream))
         torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for i in range(reps):
-            graphs[i % len(graphs)].replay()
-        end.record(stream)
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) / reps  # ms per replay
-
-    with torch.cuda.stream(stream):
-        ms_step = timed(step_graphs, args.steps)
-    print(f"[bench] step {ms_step * 1e3:.1f} us for {step_bytes / 1e6:.1f} MB of weights", file=sys.stderr, flush=True)
-
-    # Dominant kernel: Q4_K gate/up GEMV at every batch size, copies rotating.
-    name, qtype, n, k = mats[0]
-    per_m = {}
-    for m in batches:
-        x = xs[name][:m]
-        s0 = torch.cuda.current_stream().cuda_stream
-        # the activation is prepared once outside the graph; the graph holds only GEMVs
-        with torch.cuda.stream(stream):
-            native.check(lib, lib.kai_fused_prepare(x.data_ptr(), 2, m, k, k, acts[name].data_ptr(), 0,
-                                                    stream.cuda_stream))
-        del s0
-
-        def gemv_fn(m=m):
-            def fn():
-                s = torch.cuda.current_stream().cuda_stream
-                for c in [c for _ in range(ROUNDS) for c in range(COPIES)]:
-                    if m <= 8:
-                        native.check(lib, lib.kai_fused_mmvq(weights[name][c].data_ptr(), qtype, n, k, m,
-                                                             acts[name].data_ptr(), 0, outs[name].data_ptr(), 0, n, s))
-                    else:
-                        projection(name, qtype, n, k, m, c, s)
-            return fn
-        g = capture(gemv_fn())
-        with torch.cuda.stream(stream):
-            ms = timed([g], max(10, args.steps)) / (ROUNDS * COPIES)
-        per_m[m] = ms
+        kernel_us[m] = r.per_launch_us(key, qtype, n, k, m, max(10, args.steps // 4), 2, prepare=False)
     wb = weight_bytes(qtype, n, k)
-    avg_ms = float(np.mean([per_m[m] for m in batches]))
-    achieved = wb / (avg_ms * 1e-3) / 1e9
-    by_m = {str(m): {"us": round(per_m[m] * 1e3, 2), "GB/s": round(wb / (per_m[m] * 1e-3) / 1e9, 1)}
-            for m in batches}
-    print(f"[bench] Q4_K gate/up GEMV per batch: {by_m}", file=sys.stderr, flush=True)
-
-    prefill = None
-    if not args.no_prefill:
-        m = 2048
-        xp = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float16)).to(dev)
-        outp = torch.empty((m, n), dtype=torch.float32, device=dev)
-        ptrs, types, rows = groups[(name, 0)]
-        size = lib.kai_fused_mmq_workspace(0, types, rows, 1, k, m, 1)
-        scratch = torch.empty(size, dtype=torch.uint8, device=dev)
-
-        def prefill_fn():
-            s = torch.cuda.current_stream().cuda_stream
-            native.check(lib, lib.kai_fused_mmq_run(ptrs, types, rows, 1, xp.data_ptr(), 2, k, k, m,
-                                                    outp.data_ptr(), 0, 0, scratch.data_ptr(), size, 0, s))
-        g = capture(prefill_fn)
-        with torch.cuda.stream(stream):
-            ms = timed([g], 5)
-        tops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-        prefill = {"config": "Q4_K 34816x5120, M=2048 (configs[3])", "ms": round(ms, 3),
-                   "TOPS": round(tops, 2), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
-        print(f"[bench] prefill {prefill}", file=sys.stderr, flush=True)
-
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(weights[name][0], qtype, n, k, args.cpu_seconds)
-
-    # HBM bytes per launch of the same kernels, from the FETCH_SIZE / WRITE_SIZE counter runs
-    # (scaled by a plain copy's readings) summarised in profiles/.
-    traffic = None
+    avg_us = float(np.mean(list(kernel_us.values())))
+    achieved = wb / (avg_us * 1e-6) / 1e9
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": f"Q4_K gate/up 34816x5120 decode kernel, batch {','.join(map(str, decode))} "
+                      "(GEMV up to 4 rows, paired int8 MMQ tile above), activation prepared outside the timing",
+            "bytes_per_launch": wb, "avg_launch_us": round(avg_us, 2),
+            "by_batch": {str(m): {"us": round(u, 2), "GB/s": round(wb / (u * 1e-6) / 1e9, 1),
+                                  "kernel": kernel_name(qtype, m)} for m, u in kernel_us.items()}}
     tfile = ROOT / "profiles" / "gemv_q4k_34816x5120_traffic.json"
     if tfile.exists():
-        tb = json.loads(tfile.read_text())["by_batch"]
-        if all(str(m) in tb for m in batches):
-            traffic = round(float(np.mean([tb[str(m)]["bytes"] for m in batches])))
+        tb = json.loads(tfile.read_text()).get("by_batch", {})
+        if all(str(m) in tb for m in decode):
+            roof["traffic"] = round(float(np.mean([tb[str(m)]["bytes"] for m in decode])))
+            roof["traffic_source"] = f"profiles/{tfile.name} (rocprofv3 FETCH_SIZE/WRITE_SIZE, not this run)"
+    print(f"[bench] roofline {roof['by_batch']}", file=sys.stderr, flush=True)
+
+    # ---- per-config legs: whole calls
+    legs = []
+
+    def leg(cfg, mname, qtype, n, k, m, key):
+        us = r.per_launch_us(key, qtype, n, k, m, args.reps, 2)
+        wbytes = weight_bytes(qtype, n, k)
+        entry = {"config": cfg, "matrix": f"{mname} {NAMES[qtype]} {n}x{k}", "m": m, "us": round(us, 2),
+                 "kernel": kernel_name(qtype, m), "includes": "activation preparation"}
+        if m >= 512:
+            tops = 2.0 * m * n * k / (us * 1e-6) / 1e12
+            entry.update({"TOPS": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4), "bound": "mfma int8"})
+        else:
+            gbs = wbytes / (us * 1e-6) / 1e9
+            entry.update({"GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "bound": "hbm"})
+        legs.append(entry)
+        print(f"[bench] leg {entry}", file=sys.stderr, flush=True)
+
+    if "C3" in chosen:
+        for name, qtype, n, k in C3:
+            for m in batches:
+                leg("C3", name, qtype, n, k, m, ("C3", name))
+    for i, (cfg, mname, qtype, n, k, ms) in enumerate(LEGS):
+        if cfg not in chosen:
+            continue
+        key = (cfg, mname)
+        r.add(key, qtype, n, k, 2000 + i, max(ms))
+        for m in ms:
+            leg(cfg, mname, qtype, n, k, m, key)
+        del r.weights[key], r.groups[key]
+        r.ws.pop(key, None)
+        torch.cuda.empty_cache()
+
+    cpu = None if args.no_cpu else cpu_baseline(r.weights[("C3", "gate_up")][0], Q4_K, 34816, 5120, args.cpu_seconds)
 
     result = {
         "metric": "weight-stream HBM GB/s (% of peak) for Q4_K GEMV b1-16; prefill int8 TOPS",
@@ -235,14 +293,12 @@ def main():
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic: weights quantized from seeded N(0,0.02), activations fp16 N(0,1)",
-        "config": {"workload": "C3 Qwen-27B-like Q4_K/Q6_K decode GEMV, batch " + args.batches,
-                   "matrices": {nm: [n_, k_] for nm, _, n_, k_ in mats},
-                   "step_weight_bytes": step_bytes, "weight_copies": COPIES},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "Q4_K gate/up GEMV 34816x5120 (mean over batch " + args.batches + ")",
-                     "bytes_per_launch": wb, "avg_launch_us": round(avg_ms * 1e3, 2), "by_batch": by_m},
-        "prefill": prefill,
+        "config": {"workload": "C3 Qwen-27B-like Q4_K/Q6_K decode, batch " + args.batches,
+                   "matrices": {nm: [n_, k_] for nm, _, n_, k_ in C3},
+                   "step_weight_bytes": step_bytes,
+                   "weight_copies": {nm: len(r.weights[("C3", nm)]) for nm, _, _, _ in C3}},
+        "roofline": roof,
+        "legs": legs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
@@ -250,17 +306,17 @@ def main():
 
 def kernel_sample(lib, dev, batches):
     """Eager launches for rocprofv3 --pmc runs: FETCH_SIZE / WRITE_SIZE of a plain copy of
-    known size (the calibration) next to those of the Q4_K gate/up GEMV per batch size."""
+    known size (the calibration) next to those of the Q4_K gate/up decode kernel per batch."""
     import torch
 
     from kaillm_amd import native
-    from kaillm_amd.formats import Q4_K, quantize
+    from kaillm_amd.formats import quantize
 
     n, k = 34816, 5120
     g = torch.Generator(device=dev).manual_seed(1000)
     w32 = torch.randn((n, k), generator=g, device=dev, dtype=torch.float32).mul_(0.02).cpu().numpy()
     packed = torch.from_numpy(quantize(w32, Q4_K)).to(dev)
-    copies = [packed] + [packed.clone() for _ in range(COPIES - 1)]
+    copies = [packed] + [packed.clone() for _ in range(MIN_COPIES - 1)]
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -284,12 +340,23 @@ def kernel_sample(lib, dev, batches):
                 native.check(lib, lib.kai_fused_mmq_run(ptrs, types, rows, 1, x.data_ptr(), 2, k, k, m,
                                                         out.data_ptr(), 0, 0, scratch.data_ptr(), size, 0, s))
     torch.cuda.synchronize()
-    print(f"[bench] kernel sample: 3 copies of {src.numel()} bytes, Q4_K {n}x{k} GEMV x{COPIES} "
+    print(f"[bench] kernel sample: 3 copies of {src.numel()} bytes, Q4_K {n}x{k} x{MIN_COPIES} "
           f"at batch {batches}", flush=True)
 
 
+def cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(w_dev, qtype, n, k, seconds):
-    """Oracle GEMV (the C restatement of the reference arithmetic) on host cores."""
+    """The oracle's GEMV (the C restatement of the reference arithmetic, OpenMP over rows) on
+    the host cores: a bounded sample of the gate/up matrix at M=1."""
     sys.path.insert(0, str(ROOT / "tests"))
     import _oracle as O
 
@@ -308,7 +375,8 @@ def cpu_baseline(w_dev, qtype, n, k, seconds):
             break
     dt = (time.perf_counter() - t0) / reps
     wb = rows * (k // 256) * 144
-    return {"value": round(wb / dt / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+    return {"value": round(wb / dt / 1e9, 3), "unit": "GB/s", "cores": cores, "threads": cores, "kind": "port",
+            "cpu_model": cpu_model(), "build": o.oracle_build_info().decode(),
             "sample": f"oracle_mul_mat_f32 Q4_K {rows}x{k} rows of gate/up, M=1, {reps} calls in {seconds:.0f}s, "
                       f"{dt * 1e3:.2f} ms/call"}
 
