@@ -67,25 +67,33 @@ Group validate_group(const int *types, const int64_t *rows, int count, int64_t k
 
 // Scratch of one batched call, each region 256-aligned: [inverse: m fp32] then one plane
 // of GGML MMQ's activation (mmq_plane_bytes) per layout a matrix of the group reads, in the
-// order D4, DS4, D2S6.
+// order D4, DS4, D2S6, then the small-M GEMM's K-chunk partial sums (the largest any
+// matrix needs; the matrices use it in turn).
 struct MmqScratch {
-    size_t inverse = 0, plane[3] = {0, 0, 0}, total = 0;
+    size_t inverse = 0, plane[3] = {0, 0, 0}, partial = 0, partial_bytes = 0, total = 0;
     bool has_plane[3] = {false, false, false};
 };
-MmqScratch mmq_scratch(const int *types, int count, int64_t k, int64_t m) {
+MmqScratch mmq_scratch(const int *types, const int64_t *rows, int count, int64_t k, int64_t m) {
     MmqScratch p;
-    for (int i = 0; i < count; ++i) p.has_plane[kai::mmq_layout(types[i])] = true;
+    for (int i = 0; i < count; ++i) {
+        p.has_plane[kai::mmq_layout(types[i])] = true;
+        p.partial_bytes = std::max(p.partial_bytes, kai::mmq_partial_bytes(types[i], m, rows[i], k));
+    }
     size_t off = kai::align256(size_t(m) * sizeof(float));
     for (int l = 0; l < 3; ++l) {
         p.plane[l] = off;
-        if (p.has_plane[l]) off += kai::align256(kai::mmq_plane_bytes(m, k));
+        if (p.has_plane[l])
+            off += kai::align256(m <= kai::MMQS_MAX_ROWS ? kai::mmqs_image_bytes(l, k) : kai::mmq_plane_bytes(m, k));
     }
+    p.partial = off;
+    off += kai::align256(p.partial_bytes);
     p.total = off;
     return p;
 }
 
-// One batched call on a prepared scratch: one preparation writes every plane the group
-// reads, then one int8 GEMM per matrix stores its column slice.
+// One batched call on a prepared scratch: one preparation writes every plane (up to 16
+// rows: small-M image) the group reads, then one int8 GEMM per matrix stores its column
+// slice.
 void run_mmq_group(const void *const *weights, const int *types, const int64_t *rows, int count, const void *x,
                    int x_dtype, int64_t stride_x, int64_t k, int64_t m, void *dst, bool dst_bf16, int64_t ld,
                    char *scratch, const MmqScratch &plan, hipStream_t s) {
@@ -94,10 +102,12 @@ void run_mmq_group(const void *const *weights, const int *types, const int64_t *
     uint8_t *planes[3];
     for (int l = 0; l < 3; ++l)
         planes[l] = plan.has_plane[l] ? reinterpret_cast<uint8_t *>(scratch + plan.plane[l]) : nullptr;
-    kai::launch_prepare_mmq(x, x_dtype, m, k, stride_x, kai::MmqPlanes{planes[0], planes[1], planes[2], inverse}, s);
+    kai::launch_prepare_mmq(x, x_dtype, m, k, stride_x,
+                            kai::MmqPlanes{planes[0], planes[1], planes[2], inverse, m <= kai::MMQS_MAX_ROWS}, s);
     int64_t col = 0;
     for (int i = 0; i < count; ++i) {
         kai::launch_mmq_planes(types[i], weights[i], rows[i], k, m, planes[kai::mmq_layout(types[i])], inverse,
+                               reinterpret_cast<float *>(scratch + plan.partial), plan.partial_bytes,
                                static_cast<char *>(dst) + col * elem, dst_bf16, ld, s);
         col += rows[i];
     }
@@ -229,7 +239,7 @@ extern "C" size_t kai_fused_mmq_workspace(int device, const int *types, const in
         last_error.clear();
         if (device < 0) throw kai::Error("Invalid device index");
         validate_group(types, rows, count, k, m);
-        return mmq_scratch(types, count, k, m).total;
+        return mmq_scratch(types, rows, count, k, m).total;
     } catch (const std::exception &error) {
         last_error = error.what();
         return 0;
@@ -242,7 +252,7 @@ extern "C" int kai_fused_mmq_run(const void *const *weights, const int *types, c
                                  uintptr_t stream) {
     return entry([&] {
         const Group g = validate_group(types, rows, count, k, m);
-        const MmqScratch plan = mmq_scratch(types, count, k, m);
+        const MmqScratch plan = mmq_scratch(types, rows, count, k, m);
         if (!weights || !x || !dst || !scratch || scratch_bytes < plan.total || k % 4 || stride_x < k || device < 0)
             throw kai::Error("Invalid fused MMQ pointers, strides or scratch capacity");
         for (int i = 0; i < count; ++i)
@@ -301,7 +311,7 @@ extern "C" int kai_fused_mmq_run_noalloc(const void *const *weights, const int *
                                          uintptr_t stream) {
     return entry([&] {
         const Group g = validate_group(types, rows, count, k, m);
-        const MmqScratch plan = mmq_scratch(types, count, k, m);
+        const MmqScratch plan = mmq_scratch(types, rows, count, k, m);
         if (plan.total > KAI_NOALLOC_SCRATCH_BYTES)
             throw kai::Error("kai_fused_mmq_run_noalloc: this call needs " + std::to_string(plan.total) +
                              " scratch bytes, above its 16 MiB capacity; use kai_fused_mmq_run");

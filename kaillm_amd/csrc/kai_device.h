@@ -20,6 +20,39 @@ __device__ __forceinline__ T load_unaligned(const void *p) {
     __builtin_memcpy(&v, p, sizeof(T));
     return v;
 }
+template <typename T>
+__device__ __forceinline__ void store_unaligned(void *p, const T &v) {
+    __builtin_memcpy(p, &v, sizeof(T));
+}
+// LDS bytes. Loads and stores through these pointers compile to ds_read / ds_write with
+// immediate offsets (a generic pointer into LDS may be kept as a 64-bit flat address, one
+// register pair per distinct offset); gfx950 reads and writes LDS at any byte alignment.
+using lds_u8 = __attribute__((address_space(3))) uint8_t;
+// Native vectors of the sizes the kernels move (the HIP vector types have no assignment
+// to an LDS-qualified object).
+template <int BYTES> struct NativeOf;
+template <> struct NativeOf<1> { using T = uint8_t; };
+template <> struct NativeOf<2> { using T = uint16_t; };
+template <> struct NativeOf<4> { using T = uint32_t; };
+template <> struct NativeOf<8> { typedef uint32_t T __attribute__((ext_vector_type(2))); };
+template <> struct NativeOf<16> { typedef uint32_t T __attribute__((ext_vector_type(4))); };
+template <typename T>
+struct __attribute__((packed)) Packed {
+    typename NativeOf<sizeof(T)>::T v;
+};
+template <typename T>
+__device__ __forceinline__ T load_unaligned(const lds_u8 *p) {
+    return __builtin_bit_cast(T, reinterpret_cast<const __attribute__((address_space(3))) Packed<T> *>(p)->v);
+}
+template <typename T>
+__device__ __forceinline__ void store_unaligned(lds_u8 *p, const T &v) {
+    reinterpret_cast<__attribute__((address_space(3))) Packed<T> *>(p)->v =
+        __builtin_bit_cast(typename NativeOf<sizeof(T)>::T, v);
+}
+// A 16-byte aligned LDS store.
+__device__ __forceinline__ void store16(lds_u8 *p, const uint4 &v) {
+    *reinterpret_cast<__attribute__((address_space(3))) NativeOf<16>::T *>(p) = __builtin_bit_cast(NativeOf<16>::T, v);
+}
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));

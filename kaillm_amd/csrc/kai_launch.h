@@ -108,10 +108,15 @@ inline bool gemv_one_launch(int64_t m, int64_t k, int two_pass) {
 }
 void launch_mmq(int type, const void *weight, int64_t n, int64_t k, int64_t m, const block_q8_1 *y,
                 const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream);
-// The same GEMM over the batched path's activation plane of the type's layout (m > 8;
-// any k that is a whole number of the type's blocks: a short last K step is masked).
+// A batched product over the batched path's activation of the type's layout (any k that
+// is a whole number of the type's blocks): up to MMQS_MAX_ROWS rows on the small-M GEMM
+// (kai_mmqs.cuh) reading the layout's small-M image, which may need
+// mmq_partial_bytes(type, m, n, k) of scratch for K-chunk partial sums; more rows on the
+// tiled int8 GEMM (kai_mmq.cuh) reading the plane.
 void launch_mmq_planes(int type, const void *weight, int64_t n, int64_t k, int64_t m, const uint8_t *plane,
-                       const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream);
+                       const float *inverse, float *partial, size_t partial_bytes, void *dst, bool dst_bf16,
+                       int64_t stride_dst, hipStream_t stream);
+size_t mmq_partial_bytes(int type, int64_t m, int64_t n, int64_t k);
 
 // Batched path (kai_fused_mmq_run): activation planes of GGML's MMQ quantisation, one per
 // layout a matrix of the group reads (D4: Q8_0, Q6_K, IQ3_S; DS4: Q4_0, Q4_K; D2S6: Q2_K).
@@ -127,9 +132,26 @@ inline int64_t mmq_blocks128(int64_t k) { return (k + MMQ_ROW_PADDING - 1) / MMQ
 inline size_t mmq_plane_bytes(int64_t m, int64_t k) {
     return size_t(mmq_blocks128(k)) * size_t(m) * MMQ_BLOCK_BYTES;
 }
+// Up to MMQS_MAX_ROWS activation rows the preparation writes, in place of each plane, the
+// small-M GEMM's LDS image of the same quantisation (kai_mmqs.cuh copies it as is). Per K
+// step of 256 values (mmqs_image_step bytes): codes [block 8][row 16][32 bytes], octet o of
+// row r at byte 8 * (o ^ ((r >> 2) & 3)); the activation scales d8 [8][16] fp32 (D4: d, DS4
+// and D2S6: the stored fp16 d); then the min-term factors, fp32: DS4 [8][16] the stored fp16
+// d * sum q (Q4_K) followed by [8][16] d8 * sum q (Q4_0); D2S6 [16][16] one per 16 values
+// (the stored fp16 sums, d8 * sum q for the last 32 values of each 128). Rows past m and
+// blocks past K are zero.
+constexpr int MMQS_MAX_ROWS = 16;
+constexpr int MMQS_CODE_BYTES = 8 * 16 * 32, MMQS_D8_BYTES = 8 * 16 * 4;
+constexpr int mmqs_image_step(int layout) {
+    return MMQS_CODE_BYTES + MMQS_D8_BYTES + (layout == MMQ_D4 ? 0 : 2 * MMQS_D8_BYTES);
+}
+__host__ __device__ inline int64_t mmqs_steps(int64_t k) { return (k + 255) / 256; }
+inline size_t mmqs_image_bytes(int layout, int64_t k) { return size_t(mmqs_steps(k)) * mmqs_image_step(layout); }
+
 struct MmqPlanes {
     uint8_t *d4, *ds4, *d2s6;  // null when no matrix of the group reads that layout
     float *inverse;
+    bool image;  // small-M images (m <= MMQS_MAX_ROWS) instead of planes
 };
 void launch_prepare_mmq(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const MmqPlanes &planes,
                         hipStream_t stream);

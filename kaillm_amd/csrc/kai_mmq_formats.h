@@ -50,7 +50,8 @@ template <> struct MmqW<Q8_0> {
     };
     // nvalid < 8 only on a short last K step: blocks past the row end re-read its last block
     // (their activation is zero)
-    static __device__ void load(Raw &r, const uint8_t *p, int o, int nvalid) {
+    template <typename P>
+    static __device__ void load(Raw &r, P p, int o, int nvalid) {
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
             const int c = nvalid == 8 ? b : min(b, nvalid - 1);
@@ -74,7 +75,8 @@ template <> struct MmqW<Q4_0> {
         uint2 q[8];
         uint32_t d[8];
     };
-    static __device__ void load(Raw &r, const uint8_t *p, int o, int nvalid) {
+    template <typename P>
+    static __device__ void load(Raw &r, P p, int o, int nvalid) {
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
             const int c = nvalid == 8 ? b : min(b, nvalid - 1);
@@ -104,7 +106,8 @@ template <> struct MmqW<Q4_K> {
         uint4 hdr;
         uint2 q[4];
     };
-    static __device__ void load(Raw &r, const uint8_t *p, int o, int) {  // whole superblocks: no short step
+    template <typename P>  // whole superblocks: no short step
+    static __device__ void load(Raw &r, P p, int o, int) {
         r.hdr = load_unaligned<uint4>(p);
 #pragma unroll
         for (int c = 0; c < 4; ++c) r.q[c] = load_unaligned<uint2>(p + 16 + 32 * c + 8 * o);
@@ -143,7 +146,8 @@ template <> struct MmqW<Q6_K> {
         uint4 sc;
         uint32_t d;
     };
-    static __device__ void load(Raw &r, const uint8_t *p, int o, int) {  // whole superblocks: no short step
+    template <typename P>  // whole superblocks: no short step
+    static __device__ void load(Raw &r, P p, int o, int) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) r.ql[i] = load_unaligned<uint2>(p + 64 * (i / 2) + 32 * (i % 2) + 8 * o);
 #pragma unroll
@@ -185,7 +189,8 @@ template <> struct MmqW<Q2_K> {
         uint2 q[2];
         uint32_t dm;
     };
-    static __device__ void load(Raw &r, const uint8_t *p, int o, int) {  // whole superblocks: no short step
+    template <typename P>  // whole superblocks: no short step
+    static __device__ void load(Raw &r, P p, int o, int) {
         r.sc = load_unaligned<uint4>(p);
 #pragma unroll
         for (int h = 0; h < 2; ++h) r.q[h] = load_unaligned<uint2>(p + 16 + 32 * h + 8 * o);
@@ -224,7 +229,8 @@ template <> struct MmqW<IQ3_S> {
         uint32_t sc;
         uint32_t d;
     };
-    static __device__ void load(Raw &r, const uint8_t *p, int o, int) {  // whole superblocks: no short step
+    template <typename P>  // whole superblocks: no short step
+    static __device__ void load(Raw &r, P p, int o, int) {
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
             r.qs[b] = load_unaligned<uint16_t>(p + 2 + 8 * b + 2 * o);

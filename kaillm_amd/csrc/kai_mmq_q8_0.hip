@@ -1,9 +1,11 @@
-// MMQ instantiations for Q8_0 (kernel template in kai_mmq.cuh).
-#include "kai_mmq.cuh"
+// MMQ instantiations for Q8_0 (kernel templates in kai_mmq.cuh and kai_mmqs.cuh).
+#include "kai_mmqs.cuh"
 
 namespace kai {
 template void launch_mmq_type<Q8_0, false>(const void *, int64_t, int64_t, int64_t, const void *, const float *, void *,
                                        bool, int64_t, hipStream_t);
 template void launch_mmq_type<Q8_0, true>(const void *, int64_t, int64_t, int64_t, const void *, const float *, void *,
                                       bool, int64_t, hipStream_t);
+template void launch_mmqs<Q8_0>(const void *, int64_t, int64_t, int64_t, const uint8_t *, const float *, float *,
+                             size_t, void *, bool, int64_t, hipStream_t);
 }  // namespace kai

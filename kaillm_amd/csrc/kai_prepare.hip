@@ -241,19 +241,76 @@ __device__ __forceinline__ uint2 pack_codes(const int8_t (&q)[8]) {
 //   D2S6 half d of each 64 values, then half d * sum q of the 16-value groups 0..5.
 // The row scale and inverse are those of prepare_q8_1_kernel (same launch shape, same
 // arithmetic), and one launch writes every plane the group needs (null when absent).
+// One lane's share of the small-M images (layout in kai_launch.h): octet `part` of block ib
+// of row r, quantised as for the planes; lane 0 of the quad (of each 16-value pair for
+// D2S6) writes the block's scale and terms, which are the values the planes' headers
+// decode to.
+__device__ __forceinline__ void mmqs_image_lane(const MmqPlanes &p, int ib, int r, int part, const float (&v)[8]) {
+    const size_t step = static_cast<size_t>(ib >> 3);
+    const int b = ib & 7;
+    const int code_at = (b * 16 + r) * 32 + 8 * (part ^ ((r >> 2) & 3));
+    const int word_at = MMQS_CODE_BYTES + (b * 16 + r) * 4;
+    if (p.d4 || p.ds4) {
+        int8_t q[8];
+        int s;
+        const float d = mmq_group_codes<32>(v, q, s);
+        const uint2 packed = pack_codes(q);
+        const int total = quad_sum(s);
+        if (p.d4) {
+            uint8_t *img = p.d4 + step * mmqs_image_step(MMQ_D4);
+            *reinterpret_cast<uint2 *>(img + code_at) = packed;
+            if (part == 0) *reinterpret_cast<float *>(img + word_at) = d;
+        }
+        if (p.ds4) {
+            uint8_t *img = p.ds4 + step * mmqs_image_step(MMQ_DS4);
+            *reinterpret_cast<uint2 *>(img + code_at) = packed;
+            if (part == 0) {
+                const float dh = half_bits_to_float(float_to_half_bits(d));
+                float *w = reinterpret_cast<float *>(img + word_at);
+                w[0] = dh;
+                w[MMQS_D8_BYTES / 4] = half_bits_to_float(static_cast<uint16_t>(half_of_product(d, total)));
+                w[MMQS_D8_BYTES / 2] = dh * static_cast<float>(total);
+            }
+        }
+    }
+    if (p.d2s6) {
+        int8_t q[8];
+        int s;
+        const float d = mmq_group_codes<64>(v, q, s);
+        uint8_t *img = p.d2s6 + step * mmqs_image_step(MMQ_D2S6);
+        *reinterpret_cast<uint2 *>(img + code_at) = pack_codes(q);
+        const int s16 = s + dpp_i32<DPP_QUAD_1032>(s);  // lanes {0,1} and {2,3}: 16 values each
+        const float dh = half_bits_to_float(float_to_half_bits(d));
+        if (part == 0) *reinterpret_cast<float *>(img + word_at) = dh;
+        if ((part & 1) == 0) {
+            const int g = 2 * b + (part >> 1);
+            const float t = (b & 3) < 3 ? half_bits_to_float(static_cast<uint16_t>(half_of_product(d, s16)))
+                                        : dh * static_cast<float>(s16);
+            *reinterpret_cast<float *>(img + MMQS_CODE_BYTES + MMQS_D8_BYTES + (g * 16 + r) * 4) = t;
+        }
+    }
+}
+
 template <int DTYPE>
 __global__ __launch_bounds__(PREP_THREADS) void prepare_mmq_kernel(
     const typename Src<DTYPE>::T *__restrict__ x, int64_t stride_x, int k, int m, int kpad_blocks, MmqPlanes p) {
     __shared__ float wave_max_lds[PREP_THREADS / WAVE];
-    const int row = blockIdx.x;
+    const int row = blockIdx.x;  // images: rows m..15 are written as zeros
     const int nblocks = k / QK8_1;
     const int part = threadIdx.x & 3, ib = blockIdx.y * PREP_BLOCKS + (threadIdx.x >> 2);
     const auto *xr = x + static_cast<int64_t>(row) * stride_x;
-    float v[8];
-    const float scale = row_scale<DTYPE>(xr, k, wave_max_lds, p.inverse + row, blockIdx.y == 0 && threadIdx.x == 0, v);
+    float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    float scale = 0.0f;
+    if (row < m)  // uniform over the workgroup
+        scale = row_scale<DTYPE>(xr, k, wave_max_lds, p.inverse + row, blockIdx.y == 0 && threadIdx.x == 0, v);
     if (ib >= kpad_blocks) return;  // whole groups of 8 lanes (kpad_blocks is a multiple of 16)
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = ib < nblocks ? v[j] * scale : 0.0f;
+    if (p.image) {
+        if (ib >= 8 * static_cast<int>(mmqs_steps(k))) return;  // whole groups of 8 lanes
+        mmqs_image_lane(p, ib, row, part, v);
+        return;
+    }
     const int sub = ib & 3;  // 32-value block within the 128-value block
     const size_t blk = (static_cast<size_t>(ib >> 2) * static_cast<size_t>(m) + static_cast<size_t>(row)) * MMQ_BLOCK_BYTES;
     const size_t codes = blk + 16 + 32 * sub + 8 * part;
@@ -317,7 +374,8 @@ template <int DTYPE>
 static void launch_prepare_mmq_dtype(const void *x, int64_t m, int64_t k, int64_t stride_x, const MmqPlanes &p,
                                      hipStream_t stream) {
     const int kpad_blocks = static_cast<int>(mmq_blocks128(k) * 4);
-    const dim3 grid(static_cast<unsigned>(m), static_cast<unsigned>((kpad_blocks + PREP_BLOCKS - 1) / PREP_BLOCKS));
+    const int64_t rows = p.image ? MMQS_MAX_ROWS : m;  // images: the zero rows too
+    const dim3 grid(static_cast<unsigned>(rows), static_cast<unsigned>((kpad_blocks + PREP_BLOCKS - 1) / PREP_BLOCKS));
     prepare_mmq_kernel<DTYPE><<<grid, dim3(PREP_THREADS), 0, stream>>>(
         static_cast<const typename Src<DTYPE>::T *>(x), stride_x, static_cast<int>(k), static_cast<int>(m),
         kpad_blocks, p);
@@ -327,6 +385,7 @@ void launch_prepare_mmq(const void *x, int x_dtype, int64_t m, int64_t k, int64_
                         hipStream_t stream) {
     if (k % QK8_1 || k <= 0 || m <= 0 || m > INT_MAX || mmq_blocks128(k) * 4 > INT_MAX)
         throw Error("Invalid batched activation shape");
+    if (planes.image && m > MMQS_MAX_ROWS) throw Error("Small-M images hold at most 16 activation rows");
     switch (x_dtype) {
         case 0: launch_prepare_mmq_dtype<0>(x, m, k, stride_x, planes, stream); break;
         case 1: launch_prepare_mmq_dtype<1>(x, m, k, stride_x, planes, stream); break;

@@ -215,23 +215,68 @@ def host_bits(x_dev):
 
 
 def plane_offsets(m, k, layouts):
-    """Scratch offsets of kai_fused_mmq_run: [inverse][plane D4][plane DS4][plane D2S6]..."""
+    """Scratch offsets of kai_fused_mmq_run: [inverse][D4][DS4][D2S6]..., each a plane, or
+    for up to 16 rows the small-M image."""
     a256 = lambda b: (b + 255) // 256 * 256
     off = a256(4 * m)
-    plane = O.mmq_blocks128(k) * m * 144
     out = {}
     for l in (O.D4, O.DS4, O.D2S6):
         if l in layouts:
             out[l] = off
-            off += a256(plane)
+            off += a256(image_bytes(l, k) if m <= 16 else O.mmq_blocks128(k) * m * 144)
     return out
 
 
+def image_bytes(layout, k):
+    return (k + 255) // 256 * (4608 if layout == O.D4 else 5632)
+
+
+def small_m_image(plane, layout, k):
+    """The small-M image a plane [K/128][m][144] re-lays as (the layout the preparation writes
+    for up to 16 rows): per 256-value step, codes [8][16][32] with octet o of row r at byte
+    8 * (o ^ ((r >> 2) & 3)), d8 [8][16] fp32, then the terms: DS4 the stored fp16 sums and
+    d8 * sum(codes), D2S6 one per 16 values (stored sums, d8 * sum(codes) past value 96 of 128)."""
+    nb, m, _ = plane.shape
+    steps = (k + 255) // 256
+    codes = np.zeros((steps, 8, 16, 4, 8), np.uint8)
+    d8 = np.zeros((steps, 8, 16), np.float32)
+    terms = np.zeros((steps, 16, 16), np.float32)
+    for s in range(steps):
+        for b in range(8):
+            blk, sub = 2 * s + b // 4, b % 4
+            hdr = plane[blk, :, :16]
+            q = plane[blk, :, 16 + 32 * sub:48 + 32 * sub]
+            qs = q.view(np.int8).astype(np.int64)
+            for r in range(m):
+                for o in range(4):
+                    codes[s, b, r, o ^ ((r >> 2) & 3)] = q[r, 8 * o:8 * o + 8]
+            if layout == O.D4:
+                d8[s, b, :m] = hdr.copy().view(np.float32)[:, sub]
+            elif layout == O.DS4:
+                halves = hdr.copy().view(np.float16).astype(np.float32)
+                d8[s, b, :m] = halves[:, 2 * sub]
+                terms[s, b, :m] = halves[:, 2 * sub + 1]
+                terms[s, 8 + b, :m] = d8[s, b, :m] * qs.sum(axis=1).astype(np.float32)
+            else:
+                halves = hdr.copy().view(np.float16).astype(np.float32)
+                d8[s, b, :m] = halves[:, sub >> 1]
+                for g in range(2):
+                    if sub < 3:
+                        terms[s, 2 * b + g, :m] = halves[:, 2 + 2 * sub + g]
+                    else:
+                        terms[s, 2 * b + g, :m] = d8[s, b, :m] * qs[:, 16 * g:16 * g + 16].sum(axis=1).astype(np.float32)
+    nterm = 0 if layout == O.D4 else 16
+    parts = [codes.reshape(steps, -1), d8.view(np.uint8).reshape(steps, -1),
+             terms[:, :nterm].view(np.uint8).reshape(steps, -1)]
+    return np.concatenate(parts, axis=1).reshape(-1)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("m,k", [(9, 256), (17, 1056), (80, 5120), (130, 2080)])
+@pytest.mark.parametrize("m,k", [(9, 256), (12, 2080), (16, 4096), (17, 1056), (80, 5120), (130, 2080)])
 def test_mmq_planes_bit_exact(kai, dtype, m, k):
     """The batched path's activation (row scale + GGML MMQ quantisation into D4, DS4 and
-    D2S6 planes, K padded to 512) read back from the scratch equals the oracle's bytes."""
+    D2S6 planes, K padded to 512; up to 16 rows the small-M images of those planes) read
+    back from the scratch equals the oracle's bytes."""
     print(f"mmq planes dtype={dtype} m={m} k={k}", flush=True)
     rng = np.random.default_rng(m + k)
     kq = k if k % 256 == 0 else None
@@ -252,8 +297,8 @@ def test_mmq_planes_bit_exact(kai, dtype, m, k):
     got = scratch.cpu().numpy()
     for layout in layouts:
         plane, inverse = O.prepare_mmq(xs, layout, code)
-        nbytes = plane.size
-        assert np.array_equal(got[offs[layout]:offs[layout] + nbytes], plane.reshape(-1)), O.LAYOUT_NAMES[layout]
+        want = small_m_image(plane, layout, k) if m <= 16 else plane.reshape(-1)
+        assert np.array_equal(got[offs[layout]:offs[layout] + want.size], want), O.LAYOUT_NAMES[layout]
         assert np.array_equal(got[:4 * m].view(np.float32), inverse)
     assert O.normwise_rel(out.cpu().numpy(), batched_ref(mats, xs, code)) <= TOL_F32
 
