@@ -103,9 +103,9 @@ int kai_fused_mmvq(const void *weight, int type, int64_t n, int64_t k, int64_t m
 
 /* Scratch bytes kai_fused_mmq_run needs for `count` matrices (types[i], rows[i])
  * sharing k, at m > 8 activation rows: [inverse: m floats][one activation region per
- * layout the group reads, D4 then DS4 then D2S6][up to 16 rows: fp32 partial sums of K
- * chunks, at most one chunk per 256 values of k, x m x rows[i]], each region padded to
- * 256 bytes. Above 16 rows a region is a plane: 128-value blocks of 144 bytes in [k/128][m]
+ * layout the group reads, D4 then DS4 then D2S6][up to 16 rows: the small-M GEMM's fp32
+ * partial sums, 16 x 16 values per piece of a 16-row set (a few pieces per set)], each
+ * region padded to 256 bytes. Above 16 rows a region is a plane: 128-value blocks of 144 bytes in [k/128][m]
  * order with k padded to 512; up to 16 rows it is the same quantisation laid out for the
  * small-M GEMM's LDS, 4608 bytes (D4) or 5632 bytes (DS4, D2S6) per 256 values of k.
  * direct_f32 is accepted for signature compatibility (outputs are always stored in

@@ -4,22 +4,24 @@
 // Y[m, n] = inverse[m] * sum over K of the GGML MMQ block arithmetic (kai_mmq.cuh, MMA
 // flavour), i.e. the same per-block integer dots, scales and min terms as mmq_kernel.
 //
-// Design for gfx950:
-//   * the preparation writes the activation as this kernel's LDS image (kai_launch.h,
-//     MmqPlanes), so a workgroup stages its K chunk with direct global-to-LDS copies
-//     (global_load_lds_dwordx4): no registers, no conversion, one barrier;
-//   * a workgroup (WAVES waves) owns 16 * WAVES weight rows (16 per wave) and one chunk of
-//     K steps (256 values each); each wave streams its rows' wire bytes from HBM into a
-//     ring of DEPTH K steps of registers with no barrier and no branch in the loop: a
-//     chunk is a whole number of ring turns (steps past the chunk read zero activation,
-//     their weight loads are clamped to the chunk's last step), so every load and wait is
-//     straight-line code;
+// Design for gfx950. At 16 rows the whole product is a few tens of K steps per SIMD, so a
+// wave's start-up (its first weight loads from HBM) costs as much as its work unless each
+// wave starts once; the kernel is therefore persistent and stream-K balanced:
+//   * one workgroup of 16 waves per CU (MMQS_GRID of them); K is cut into as few chunks as
+//     the LDS holds (usually one), and each chunk's workgroups stage its activation once,
+//     from the LDS image the preparation wrote (kai_launch.h, MmqPlanes), with direct
+//     global-to-LDS copies (global_load_lds_dwordx4): no registers, one barrier;
+//   * a chunk's work is the row-major sequence of (16-row set, K step) pairs; its waves take
+//     equal contiguous runs of it, so every SIMD gets the same number of steps whatever the
+//     shape. A run crosses row sets: the wave's ring of DEPTH steps of weight loads runs on
+//     across them, and at the end of each piece of a row set the wave stores its sums;
+//   * weights stream as contiguous 16-byte units per row into the wave's LDS transpose
+//     buffer (MmqsStream), from which each lane reads its MFMA operand fields;
 //   * per 32-value block one v_mfma_i32_16x16x32_i8 (two for formats with per-16 scales),
 //     the fp32 epilogue of the block's scales, min terms on v_mfma_f32_16x16x4f32;
-//   * K is split into chunks when the rows alone leave the chip short of workgroups or a
-//     whole row's activation would not fit the LDS; each chunk writes fp32 partial sums
-//     [chunk][m][n] that mmqs_reduce_kernel adds in chunk order (deterministic), times
-//     inverse, into the strided output.
+//   * each piece of a row set goes to fp32 partial sums [chunk][row set][piece][16][16]
+//     that mmqs_reduce_kernel adds in chunk and piece order (deterministic), times inverse,
+//     into the output.
 #pragma once
 
 #include <type_traits>
@@ -28,9 +30,10 @@
 
 namespace kai {
 
-constexpr int MMQS_DEPTH = 2, MMQS_WAVES = 4;
-constexpr int MMQS_LDS_BUDGET = 40 * 1024;  // per workgroup: four workgroups per CU
-static_assert(MMQS_LDS_BUDGET <= 64 * 1024, "the launch does not raise the dynamic LDS limit");
+constexpr int MMQS_DEPTH = 2, MMQS_WAVES = 16;
+constexpr int MMQS_GRID = 256;              // workgroups: one per CU of an MI355X
+constexpr int MMQS_LDS_BUDGET = 160 * 1024;  // the CU's LDS
+constexpr int MMQS_MIN_RUN = 4;             // K steps a wave takes at least (when it has work)
 
 template <int TYPE>
 constexpr int mmqs_step_bytes() {  // one K step of 16 activation rows in LDS
@@ -39,14 +42,15 @@ constexpr int mmqs_step_bytes() {  // one K step of 16 activation rows in LDS
 
 // One K step of one wave: 8 blocks x (1 or 2) int8 MFMAs against the staged activation at
 // `base`, the block epilogue, and the min terms. Batched (MMA) arithmetic of the format.
-// Each half step (4 blocks) runs in phases: operand reads and codes, then the MFMAs, then
+// Each group of HALF blocks runs in phases: operand reads and codes, then the MFMAs, then
 // the epilogues, so every MFMA's latency is covered by the other blocks' work.
 template <int TYPE>
 __device__ __forceinline__ void mmqs_step(typename MmqW<TYPE>::Raw &w, const uint8_t *base, v4f_t &acc, int col,
                                           int oct, int aoct, const uint32_t *grid) {
     using W = MmqLoad<TYPE>;
     constexpr int MODE = W::template mode<true>();
-    constexpr int MT = 16, NT = W::NTERM, HALF = 4;
+    // blocks per phase: their MFMA results, operands and scales are live at once
+    constexpr int MT = 16, NT = W::NTERM, HALF = MODE == MMQ_BLOCK ? 4 : 2;
     constexpr int D8_OFF = MT * 8 * 32, TA_OFF = D8_OFF + MT * 8 * 4;
     const float *d8s = reinterpret_cast<const float *>(base + D8_OFF);
     const v4i_t zero = {0, 0, 0, 0};
@@ -98,7 +102,7 @@ __device__ __forceinline__ void mmqs_step(typename MmqW<TYPE>::Raw &w, const uin
                 }
             }
         }
-        __builtin_amdgcn_sched_barrier(0);  // one half step's results live at a time
+        __builtin_amdgcn_sched_barrier(0);  // one phase's results live at a time
     }
     if constexpr (NT > 0) {
         const float *ta = reinterpret_cast<const float *>(base + TA_OFF);
@@ -122,208 +126,252 @@ struct MmqsStream {
     static constexpr int UPL = (16 * U + WAVE - 1) / WAVE;  // units per lane
 };
 
-// grid: x = blocks of 16 * WAVES weight rows, y = K chunks of `chunk` steps; the ring runs
-// over `span` steps (chunk rounded up to a multiple of DEPTH; the padding reads zero
-// activation). partial: [gridDim.y][m][n] fp32 when gridDim.y > 1, else the output is stored
-// directly.
+// The work split of a launch (host and device agree on it).
+struct MmqsSplit {
+    int chunks, chunk;  // K chunks of `chunk` steps (the last may be shorter)
+    int wgs;            // workgroups per chunk
+    int waves;          // waves per chunk that take work
+    int qmax;           // pieces a row set has at most in one chunk
+};
+// Steps of chunk c; its positions per row set (rounded up to even: an odd chunk gets a zero
+// step); and the run of its waves (even). With both even every piece of a row set starts at
+// an even position and has an even length, so the loop runs whole ring turns (DEPTH 2).
+__host__ __device__ inline int mmqs_chunk_steps(const MmqsSplit &p, int steps, int c) {
+    return min(p.chunk, steps - c * p.chunk);
+}
+__host__ __device__ inline int mmqs_positions(int sc) { return sc + (sc & 1); }
+__host__ __device__ inline int mmqs_run(const MmqsSplit &p, int rowsets, int sc) {
+    const int run = (rowsets * mmqs_positions(sc) + p.waves - 1) / p.waves;
+    return run + (run & 1);
+}
+
+// grid: chunks * wgs workgroups of WAVES waves; workgroup b works on chunk b / wgs.
 template <int TYPE, int DEPTH, int WAVES>
 __global__ __launch_bounds__(WAVES * WAVE) void mmqs_kernel(
     const uint8_t *weight, int64_t row_bytes, int n, int k, const uint8_t *__restrict__ image, int m,
-    const float *__restrict__ inverse, int chunk, int span, float *__restrict__ partial, void *__restrict__ dst,
+    const float *__restrict__ inverse, MmqsSplit split, float *__restrict__ partial, void *__restrict__ dst,
     int64_t stride_dst, int dst_bf16) {
     constexpr int THREADS = WAVES * WAVE;
     // `weight` is not __restrict__: its loads must stay ordered by the compiler fences of the
     // ring below (loads through a restrict pointer are treated as invariant and move freely)
     using W = MmqLoad<TYPE>;
+    using S = MmqsStream<TYPE>;
     constexpr int BUF = mmqs_step_bytes<TYPE>(), IMG = mmqs_image_step(mmq_layout(TYPE));
     constexpr int UNITS = BUF / 16;  // 16-byte units of one staged step
     extern __shared__ __align__(16) uint8_t kai_mmqs_lds[];
     __shared__ uint32_t grid_lds[TYPE == IQ3_S ? 512 : 1];
 
-    const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
+    const int tid = threadIdx.x, lane = tid % WAVE;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);  // uniform: the run's control is scalar
     const int col = lane % 16, oct = lane / 16;
     const int nb = k / QK8_1, steps = (k + MMQ_STEP - 1) / MMQ_STEP;
-    const int s0 = blockIdx.y * chunk, own = min(chunk, steps - s0);  // this chunk's real steps
-    const int nrow0 = (blockIdx.x * WAVES + wave) * 16;
+    const int chunk_id = blockIdx.x / split.wgs;
+    const int s0 = chunk_id * split.chunk, sc = mmqs_chunk_steps(split, steps, chunk_id);
+    const int rowsets = (n + 15) / 16;
+    // this wave's run [t0, t1) of the chunk's (row set, step) sequence
+    const int w = (blockIdx.x % split.wgs) * WAVES + wave;
+    const int sce = mmqs_positions(sc), run = mmqs_run(split, rowsets, sc), total = rowsets * sce;
+    const int t0 = w < split.waves ? min(w * run, total) : total, t1 = w < split.waves ? min(t0 + run, total) : total;
     if constexpr (TYPE == IQ3_S) {
         for (int i = tid; i < 512; i += THREADS) grid_lds[i] = mmq_iq3s_grid[i];
     }
 
-    // ---- the lane's units (row r = u / U, unit c = u % U of the wave's rows), as 32-bit byte
+    // ---- the lane's units (row r = u / U, unit c = u % U of a row set), as 32-bit byte
     // offsets into the matrix (the launcher checks that it is below 4 GiB), so every load is
-    // the step's scalar base plus a fixed lane offset; a lane with no unit in a group re-reads
-    // the wave's first unit into a spare slot. A wave whose last row's run can end inside a
-    // unit (superblocks that are not whole units, or a short last step) clamps each unit start
-    // to the matrix's last 16 bytes and moves the unit's LDS position back by as many bytes
-    // (its bytes past the end do not exist and are never read), so no load leaves the matrix.
-    // That wave runs its own copy of the loop, so the loop body has no branch.
-    using S = MmqsStream<TYPE>;
+    // a scalar base (row set, step) plus a fixed lane offset; a lane with no unit in a group
+    // re-reads the row set's first unit into a spare slot. A wave whose run reaches the last
+    // row set, when its rows or runs can end inside a unit (rows not a multiple of 16,
+    // superblocks that are not whole units, a short last step), clamps each unit start to the
+    // matrix's last 16 bytes and moves the unit's LDS position back by as many bytes (0 for a
+    // unit wholly past the end, whose rows are never stored), so no load leaves the matrix.
+    // That wave runs its own copy of the loop, so the loop body has no branch for it.
     uint32_t ug[S::UPL];
     int uoff[S::UPL];
 #pragma unroll
     for (int i = 0; i < S::UPL; ++i) {
         const int u = lane + WAVE * i, r = u / S::U, c = u % S::U;
         const bool real = u < 16 * S::U;
-        ug[i] = real ? static_cast<uint32_t>(min(nrow0 + r, n - 1)) * static_cast<uint32_t>(row_bytes) + 16 * c
-                     : static_cast<uint32_t>(min(nrow0, n - 1)) * static_cast<uint32_t>(row_bytes);
+        ug[i] = real ? static_cast<uint32_t>(r) * static_cast<uint32_t>(row_bytes) + 16 * c : 0u;
         uoff[i] = real ? r * S::SBP + 16 * c : 16 * S::SBP;
     }
-    const bool careful = (S::SB % 16 != 0 || k % MMQ_STEP != 0) && nrow0 + 15 >= n - 1;  // uniform
+    const bool ragged = n % 16 != 0 || S::SB % 16 != 0 || k % MMQ_STEP != 0;
+    const bool careful = ragged && t1 > t0 && (t1 - 1) / sce == rowsets - 1;  // uniform
     const uint32_t tail = static_cast<uint32_t>(int64_t(n) * row_bytes - 16);
-    const int last = s0 + own - 1;  // the ring's run-ahead re-reads this (cached) step
+    const uint32_t set_bytes = 16u * static_cast<uint32_t>(row_bytes);
     struct Slot {
         uint4 v[S::UPL];
         uint32_t back;  // careful: 4 bits per unit, the bytes its load start was moved back
     };
     Slot wr[DEPTH];
-    auto wload = [&](Slot &w, int j, auto careful_tag) {
-        const uint32_t soff = static_cast<uint32_t>(min(s0 + j, last)) * S::SB;
+    // The next position to load (row set lr, position lj); the ring's run-ahead past the
+    // run's end repeats its last position, and a chunk's zero step re-reads its last step.
+    int lt = t0, lr = t1 > t0 ? t0 / sce : 0, lj = t1 > t0 ? t0 % sce : 0;
+    auto wload = [&](Slot &sl, auto careful_tag) {
+        const uint32_t lbase = static_cast<uint32_t>(lr) * set_bytes + static_cast<uint32_t>(s0 + min(lj, sc - 1)) * S::SB;
         if constexpr (decltype(careful_tag)::value) {
-            w.back = 0;
+            sl.back = 0;
 #pragma unroll
             for (int i = 0; i < S::UPL; ++i) {
-                const uint32_t g = ug[i] + soff, a = min(g, tail);
-                w.v[i] = load_unaligned<uint4>(weight + a);
-                w.back |= (g - a) << (4 * i);
+                const uint32_t g = ug[i] + lbase, a = min(g, tail), back = g - a;
+                sl.v[i] = load_unaligned<uint4>(weight + a);
+                sl.back |= (back < 16u ? back : 0u) << (4 * i);
             }
         } else {
-            const uint8_t *base = weight + soff;
+            const uint8_t *b = weight + lbase;
 #pragma unroll
-            for (int i = 0; i < S::UPL; ++i) w.v[i] = load_unaligned<uint4>(base + ug[i]);
+            for (int i = 0; i < S::UPL; ++i) sl.v[i] = load_unaligned<uint4>(b + ug[i]);
         }
+        // advance (scalar selects: a branch here would split the loop body)
+        const int adv = lt < t1 - 1 ? 1 : 0;
+        lt += adv;
+        lj += adv;
+        const int wrap = lj == sce ? 1 : 0;
+        lj = wrap ? 0 : lj;
+        lr += wrap;
     };
     auto prologue = [&](auto careful_tag) {
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
-            wload(wr[d], d, careful_tag);
+            wload(wr[d], careful_tag);
             __asm__ volatile("" ::: "memory");  // the loop's order: its waits then count the slots in flight
         }
     };
-    if (careful) prologue(std::true_type{});
-    else prologue(std::false_type{});
+    // the clamped form for every wave (it clamps nothing where the fast form is safe), so the
+    // ring enters either copy of the loop from one code path
+    if (t1 > t0) prologue(std::true_type{});
 
     // ---- the chunk's activation image -> LDS, 16 bytes a lane, a wave's 64 lanes filling
-    // 1 KiB in lane order; the ring padding past the chunk is zeroed. Q4_0 takes its terms
-    // from the image's second term array.
+    // 1 KiB in lane order. Q4_0 takes its terms from the image's second term array.
     const uint8_t *img = image + int64_t(s0) * IMG;
-    const int units = span * UNITS;
+    const int units = sc * UNITS;
     for (int u0 = wave * WAVE; u0 < units; u0 += THREADS) {
         const int u = u0 + lane, j = u / UNITS, o = (u % UNITS) * 16;
         if (u < units) {
-            if (j < own) {
-                const int src = TYPE == Q4_0 && o >= MMQS_CODE_BYTES + MMQS_D8_BYTES ? o + MMQS_D8_BYTES : o;
-                __builtin_amdgcn_global_load_lds(
-                    static_cast<const void *>(img + j * IMG + src),
-                    (__attribute__((address_space(3))) uint8_t *)kai_mmqs_lds + u0 * 16,
-                    16, 0, 0);
-            } else {
-                *reinterpret_cast<uint4 *>(kai_mmqs_lds + u * 16) = make_uint4(0, 0, 0, 0);
-            }
+            const int src = TYPE == Q4_0 && o >= MMQS_CODE_BYTES + MMQS_D8_BYTES ? o + MMQS_D8_BYTES : o;
+            __builtin_amdgcn_global_load_lds(static_cast<const void *>(img + j * IMG + src),
+                                             (__attribute__((address_space(3))) uint8_t *)kai_mmqs_lds + u0 * 16,
+                                             16, 0, 0);
         }
+    }
+    if (sce > sc) {  // the zero step of an odd chunk
+        for (int u = tid; u < UNITS; u += THREADS) store16((lds_u8 *)kai_mmqs_lds + (units + u) * 16, make_uint4(0, 0, 0, 0));
     }
     __syncthreads();
+    if (t1 <= t0) return;
 
-    // ---- stream the weights: DEPTH steps in flight, straight-line loads and waits
+    // ---- the run: DEPTH steps in flight, straight-line loads and waits; a piece of a row
+    // set ends at its last step or the run's, and is stored there
     const int aoct = W::act_pos(oct) / 8;
-    lds_u8 *tb = (lds_u8 *)kai_mmqs_lds + span * BUF + wave * (16 * S::SBP + 16);
-    auto run = [&](auto careful_tag) {
-        v4f_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int j0 = 0; j0 < span; j0 += DEPTH) {
-#pragma unroll
-            for (int d = 0; d < DEPTH; ++d) {
-                const Slot &w = wr[d];
-#pragma unroll
-                for (int i = 0; i < S::UPL; ++i) {
-                    if constexpr (decltype(careful_tag)::value)
-                        store_unaligned(tb + uoff[i] - int((w.back >> (4 * i)) & 15u), w.v[i]);
-                    else
-                        store16(tb + uoff[i], w.v[i]);
-                }
-                typename W::Raw raw;
-                W::load(raw, tb + col * S::SBP, oct, min(8, nb - 8 * min(s0 + j0 + d, last)));
-                mmqs_step<TYPE>(raw, kai_mmqs_lds + (j0 + d) * BUF, acc, col, oct, aoct, grid_lds);
-                wload(wr[d], j0 + d + DEPTH, careful_tag);
-                // keep the refill here and each step's work in its own section: without these
-                // fences the loads are sunk to their use and the next slot's decode is hoisted
-                // into this one, and the waits drain the ring every step
-                __asm__ volatile("" ::: "memory");
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-        return acc;
+    const int buf_off = mmqs_positions(split.chunk) * BUF;  // the transpose buffers follow the largest chunk
+    lds_u8 *tb = (lds_u8 *)kai_mmqs_lds + buf_off + wave * (16 * S::SBP + 16);
+    // piece q of row set r is this wave's index minus that of the wave holding the set's
+    // first step; it goes to partial [chunk][row set][q] as [16 columns][16 rows] fp32, one
+    // 16-byte store per lane
+    auto store = [&](const v4f_t &acc, int r) {
+        const int q = w - (r * sce) / run;
+        float *p = partial + (((int64_t(chunk_id) * rowsets + r) * split.qmax + q) * 16 + col) * 16 + 4 * oct;
+        *reinterpret_cast<float4 *>(p) = make_float4(acc[0], acc[1], acc[2], acc[3]);
     };
-    const v4f_t acc = careful ? run(std::true_type{}) : run(std::false_type{});
-
-    // ---- store: rows 4*oct + i of weight row nrow0 + col
-    const int c = nrow0 + col;
-    if (c >= n) return;
+    auto loop = [&](auto careful_tag) {
+#pragma unroll 1
+        for (int pa = t0; pa < t1;) {  // one piece of a row set: positions [pa, pb), both even
+            const int r = pa / sce, pb = min(t1, (r + 1) * sce);
+            v4f_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 1
+            for (int j = pa - r * sce; j < pb - r * sce; j += DEPTH) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int row = 4 * oct + i;
-        if (row >= m) continue;
-        if (gridDim.y > 1) {
-            partial[(int64_t(blockIdx.y) * m + row) * n + c] = acc[i];
-        } else {
-            const float v = acc[i] * inverse[row];
-            const int64_t idx = int64_t(row) * stride_dst + c;
-            if (dst_bf16) static_cast<uint16_t *>(dst)[idx] = float_to_bf16_bits(v);
-            else static_cast<float *>(dst)[idx] = v;
+                for (int d = 0; d < DEPTH; ++d) {
+                    const Slot &sl = wr[d];
+#pragma unroll
+                    for (int i = 0; i < S::UPL; ++i) {
+                        if constexpr (decltype(careful_tag)::value)
+                            store_unaligned(tb + uoff[i] - int((sl.back >> (4 * i)) & 15u), sl.v[i]);
+                        else
+                            store16(tb + uoff[i], sl.v[i]);
+                    }
+                    typename W::Raw raw;
+                    W::load(raw, tb + col * S::SBP, oct, min(8, nb - 8 * (s0 + min(j + d, sc - 1))));
+                    mmqs_step<TYPE>(raw, kai_mmqs_lds + (j + d) * BUF, acc, col, oct, aoct, grid_lds);
+                    wload(wr[d], careful_tag);
+                    // keep the refill here and each step's work in its own section: without
+                    // these fences the loads are sunk to their use and the next slot's decode
+                    // is hoisted into this one, and the waits drain the ring every step
+                    __asm__ volatile("" ::: "memory");
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            store(acc, r);
+            pa = pb;
         }
-    }
+    };
+    if (careful) loop(std::true_type{});
+    else loop(std::false_type{});
 }
 
-// out[row][c] = inverse[row] * sum over chunks (in order) of partial[chunk][row][c].
-static __global__ __launch_bounds__(256) void mmqs_reduce_kernel(const float *__restrict__ partial, int chunks, int m,
-                                                          int n, const float *__restrict__ inverse,
-                                                          void *__restrict__ dst, int64_t stride_dst, int dst_bf16) {
+// out[row][c] = inverse[row] * sum over chunks, then pieces (in order), of the partial sums
+// of c's row set.
+static __global__ __launch_bounds__(256) void mmqs_reduce_kernel(const float *__restrict__ partial, MmqsSplit split,
+                                                                  int steps, int m, int n,
+                                                                  const float *__restrict__ inverse,
+                                                                  void *__restrict__ dst, int64_t stride_dst,
+                                                                  int dst_bf16) {
     const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
     if (i >= int64_t(m) * n) return;
-    const int row = static_cast<int>(i / n), c = static_cast<int>(i % n);
-    float s = partial[i];
-    for (int g = 1; g < chunks; ++g) s += partial[int64_t(g) * m * n + i];
+    const int row = static_cast<int>(i / n), c = static_cast<int>(i % n), r = c / 16;
+    const int rowsets = (n + 15) / 16;
+    float s = 0.0f;
+    for (int ch = 0; ch < split.chunks; ++ch) {
+        const int sc = mmqs_chunk_steps(split, steps, ch), sce = mmqs_positions(sc), run = mmqs_run(split, rowsets, sc);
+        const int first = (r * sce) / run, last = (r * sce + sce - 1) / run;
+        const float *p = partial + ((int64_t(ch) * rowsets + r) * split.qmax * 16 + c % 16) * 16 + row;
+        for (int q = 0; q <= last - first; ++q) s += p[q * 256];
+    }
     const float v = s * inverse[row];
     const int64_t idx = int64_t(row) * stride_dst + c;
     if (dst_bf16) static_cast<uint16_t *>(dst)[idx] = float_to_bf16_bits(v);
     else static_cast<float *>(dst)[idx] = v;
 }
 
-// Launch shape: K chunk (steps staged per workgroup) and chunk count. The staged chunk and
-// the waves' transpose buffers fit MMQS_LDS_BUDGET, and K is cut into more chunks while the
-// workgroups would not fill the chip. The plan depends only on the type and shape, so the
-// scratch query and the launch agree on every device.
-struct MmqsPlan {
-    int chunk, chunks, span;
-    size_t lds;
-};
+// The split: K in as few chunks as the LDS holds (the staged chunk plus the waves' transpose
+// buffers), MMQS_GRID workgroups shared by the chunks, and runs of at least MMQS_MIN_RUN
+// steps. It depends only on the type and shape, so the scratch query and the launch agree.
 template <int TYPE>
-constexpr size_t mmqs_stream_lds() {  // per wave: 16 rows and a spare unit
+constexpr size_t mmqs_stream_lds() {  // per workgroup: 16 rows and a spare unit per wave
     return size_t(MMQS_WAVES) * (16 * MmqsStream<TYPE>::SBP + 16);
 }
 template <int TYPE>
-inline MmqsPlan mmqs_plan(int64_t n, int64_t k) {
-    constexpr int64_t WANT = 1024;  // workgroups that fill 256 CUs four deep
+inline MmqsSplit mmqs_split(int64_t n, int64_t k) {
     constexpr int BUF = mmqs_step_bytes<TYPE>();
-    constexpr int MAX_SPAN = int((MMQS_LDS_BUDGET - mmqs_stream_lds<TYPE>()) / BUF) / MMQS_DEPTH * MMQS_DEPTH;
-    static_assert(MAX_SPAN >= MMQS_DEPTH, "the LDS budget must hold one ring turn of activation");
-    const int steps = static_cast<int>(mmqs_steps(k));
-    const int64_t blocks = (n + 16 * MMQS_WAVES - 1) / (16 * MMQS_WAVES);
-    int chunks = (steps + MAX_SPAN - 1) / MAX_SPAN;
-    while (blocks * chunks < WANT && (steps + chunks) / (chunks + 1) >= 2) ++chunks;
-    MmqsPlan p;
-    p.chunk = (steps + chunks - 1) / chunks;
+    constexpr int MAX_CHUNK =  // even, so that an odd chunk's zero step fits too
+        int((MMQS_LDS_BUDGET - mmqs_stream_lds<TYPE>() - (TYPE == IQ3_S ? 2048 : 0)) / BUF) / 2 * 2;
+    static_assert(MAX_CHUNK >= 2, "the LDS must hold two K steps of activation");
+    const int steps = static_cast<int>(mmqs_steps(k)), rowsets = static_cast<int>((n + 15) / 16);
+    MmqsSplit p;
+    p.chunks = (steps + MAX_CHUNK - 1) / MAX_CHUNK;
+    p.chunk = (steps + p.chunks - 1) / p.chunks;
     p.chunks = (steps + p.chunk - 1) / p.chunk;
-    p.span = (p.chunk + MMQS_DEPTH - 1) / MMQS_DEPTH * MMQS_DEPTH;
-    p.lds = size_t(p.span) * BUF + mmqs_stream_lds<TYPE>();
+    p.wgs = std::max(1, MMQS_GRID / p.chunks);
+    const int64_t work = int64_t(rowsets) * mmqs_positions(p.chunk);  // the largest chunk's
+    p.waves = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(int64_t(p.wgs) * MMQS_WAVES,
+                                                                         work / MMQS_MIN_RUN)));
+    p.qmax = 1;
+    for (int c = 0; c < p.chunks; ++c) {
+        const int sc = mmqs_chunk_steps(p, steps, c), run = mmqs_run(p, rowsets, sc);
+        p.qmax = std::max(p.qmax, (mmqs_positions(sc) + run - 1) / run + 1);
+    }
     return p;
 }
+template <int TYPE>
+inline size_t mmqs_lds_bytes(const MmqsSplit &p) {
+    return size_t(mmqs_positions(p.chunk)) * mmqs_step_bytes<TYPE>() + mmqs_stream_lds<TYPE>();
+}
 
-// Partial-sum bytes of an m-row product with this matrix on the small-M GEMM (0 when its
-// plan has one chunk).
+// Partial-sum bytes of an m-row product with this matrix on the small-M GEMM.
 template <int TYPE>
 inline size_t mmqs_partial_bytes(int64_t m, int64_t n, int64_t k) {
     if (m < 1 || m > MMQS_MAX_ROWS) return 0;
-    const MmqsPlan p = mmqs_plan<TYPE>(n, k);
-    return p.chunks > 1 ? size_t(p.chunks) * size_t(m) * size_t(n) * sizeof(float) : 0;
+    const MmqsSplit p = mmqs_split<TYPE>(n, k);
+    return size_t(p.chunks) * size_t((n + 15) / 16) * size_t(p.qmax) * 256 * sizeof(float);
 }
 
 // image: the layout's small-M image (kai_launch.h) of the m activation rows.
@@ -332,23 +380,24 @@ void launch_mmqs(const void *weight, int64_t n, int64_t k, int64_t m, const uint
                  float *partial, size_t partial_bytes, void *dst, bool dst_bf16, int64_t stride_dst,
                  hipStream_t stream) {
     if (m < 1 || m > MMQS_MAX_ROWS) throw Error("The small-M GEMM takes 1..16 activation rows");
-    const MmqsPlan p = mmqs_plan<TYPE>(n, k);
-    const size_t need = p.chunks > 1 ? size_t(p.chunks) * size_t(m) * size_t(n) * sizeof(float) : 0;
-    if (need > partial_bytes || (need && !partial)) throw Error("Scratch too small for the small-M GEMM's partial sums");
+    if (n < 1 || k < MMQ_STEP / 8) throw Error("Invalid small-M GEMM shape");
+    const MmqsSplit p = mmqs_split<TYPE>(n, k);
+    const size_t need = mmqs_partial_bytes<TYPE>(m, n, k);
+    if (need > partial_bytes || !partial) throw Error("Scratch too small for the small-M GEMM's partial sums");
     const int64_t row_bytes = (k / block_elems(TYPE)) * block_bytes(TYPE);
     if (n * row_bytes >= (int64_t(1) << 32)) throw Error("The small-M GEMM takes matrices below 4 GiB");
-    const size_t lds = p.lds;
-    auto kernel = mmqs_kernel<TYPE, MMQS_DEPTH, MMQS_WAVES>;  // within the default 64 KiB of dynamic LDS
-    const dim3 grid(static_cast<unsigned>((n + 16 * MMQS_WAVES - 1) / (16 * MMQS_WAVES)), static_cast<unsigned>(p.chunks));
-    kernel<<<grid, MMQS_WAVES * WAVE, lds, stream>>>(static_cast<const uint8_t *>(weight), row_bytes,
-                                                     static_cast<int>(n), static_cast<int>(k), image,
-                                                     static_cast<int>(m), inverse, p.chunk, p.span, partial, dst,
-                                                     stride_dst, dst_bf16 ? 1 : 0);
-    if (p.chunks > 1) {
-        const int64_t total = m * n;
-        mmqs_reduce_kernel<<<static_cast<unsigned>((total + 255) / 256), 256, 0, stream>>>(
-            partial, p.chunks, static_cast<int>(m), static_cast<int>(n), inverse, dst, stride_dst, dst_bf16 ? 1 : 0);
-    }
+    const size_t lds = mmqs_lds_bytes<TYPE>(p);
+    auto kernel = mmqs_kernel<TYPE, MMQS_DEPTH, MMQS_WAVES>;
+    static DeviceFlags lds_raised;
+    raise_dynamic_lds(reinterpret_cast<const void *>(kernel), MMQS_LDS_BUDGET - (TYPE == IQ3_S ? 2048 : 0), lds_raised,
+                      "Cannot raise the small-M GEMM's dynamic LDS limit");
+    kernel<<<dim3(static_cast<unsigned>(p.chunks * p.wgs)), MMQS_WAVES * WAVE, lds, stream>>>(
+        static_cast<const uint8_t *>(weight), row_bytes, static_cast<int>(n), static_cast<int>(k), image,
+        static_cast<int>(m), inverse, p, partial, dst, stride_dst, dst_bf16 ? 1 : 0);
+    const int64_t total = m * n;
+    mmqs_reduce_kernel<<<static_cast<unsigned>((total + 255) / 256), 256, 0, stream>>>(
+        partial, p, static_cast<int>(mmqs_steps(k)), static_cast<int>(m), static_cast<int>(n), inverse, dst,
+        stride_dst, dst_bf16 ? 1 : 0);
 }
 
 }  // namespace kai
