@@ -24,6 +24,8 @@ HIP_FLAGS = [
     # MFMA results straight into VGPRs: the MMQ epilogue scales every MFMA output on the
     # VALU, and the AGPR form would add a v_accvgpr_read per element
     "-mllvm", "-amdgpu-mfma-vgpr-form",
+    # per-kernel register and scratch report, checked below
+    "-Rpass-analysis=kernel-resource-usage",
 ]
 CXX_FLAGS = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-pthread"]
 
@@ -43,6 +45,20 @@ def _run(cmd):
     return text
 
 
+def _check_no_scratch(text, src):
+    """Every kernel must be free of register spills: the small-M GEMM returned wrong sums
+    from its later waves whenever it spilled (its workgroups are 16 waves with up to 160 KiB
+    of LDS), so a spill anywhere fails the build instead of shipping."""
+    name = None
+    for line in text.splitlines():
+        if "Function Name:" in line:
+            name = line.split("Function Name:")[1].split("[-Rpass")[0].strip()
+        elif "ScratchSize [bytes/lane]:" in line:
+            size = int(line.split("ScratchSize [bytes/lane]:")[1].split("[")[0])
+            if size:
+                raise RuntimeError(f"{src.name}: kernel {name} spills {size} bytes per lane to scratch")
+
+
 def build(jobs=None, verbose=False):
     """Compile every source and link kaillm_amd/libkai_hip.so. Returns its path."""
     hip, cpp = _sources()
@@ -59,7 +75,10 @@ def build(jobs=None, verbose=False):
         cmds.append([shutil.which("g++") or "g++", *CXX_FLAGS, "-c", str(src), "-o", str(obj)])
         objs.append(obj)
     with cf.ThreadPoolExecutor(jobs) as pool:
-        for text in pool.map(_run, cmds):
+        for src, text in zip(hip + cpp, pool.map(_run, cmds)):
+            if src.suffix == ".hip":
+                _check_no_scratch(text, src)
+                text = "\n".join(l for l in text.splitlines() if "kernel-resource-usage" not in l and "|" not in l)
             if verbose and text:
                 print(text)
     tmp = OUT.with_suffix(".so.tmp")

@@ -66,9 +66,9 @@ Group validate_group(const int *types, const int64_t *rows, int count, int64_t k
 }
 
 // Scratch of one batched call, each region 256-aligned: [inverse: m fp32] then one plane
-// of GGML MMQ's activation (mmq_plane_bytes) per layout a matrix of the group reads, in the
-// order D4, DS4, D2S6, then the small-M GEMM's K-chunk partial sums (the largest any
-// matrix needs; the matrices use it in turn).
+// of GGML MMQ's activation (mmq_plane_bytes; up to 16 rows the small-M image) per layout a
+// matrix of the group reads, in the order D4, DS4, D2S6, then the small-M GEMM's partial
+// sums (the largest any matrix needs; the matrices use it in turn).
 struct MmqScratch {
     size_t inverse = 0, plane[3] = {0, 0, 0}, partial = 0, partial_bytes = 0, total = 0;
     bool has_plane[3] = {false, false, false};

@@ -49,15 +49,19 @@ template <> struct MmqW<Q8_0> {
         uint32_t d[8];
     };
     // nvalid < 8 only on a short last K step: blocks past the row end re-read its last block
-    // (their activation is zero)
+    // (their activation is zero). Blocks are independent, so a caller may load them one at a
+    // time (LAZY) right before their use.
+    static constexpr bool LAZY = true;
+    template <typename P>
+    static __device__ void load_block(Raw &r, P p, int o, int nvalid, int b) {
+        const int c = nvalid == 8 ? b : min(b, nvalid - 1);
+        r.d[b] = load_unaligned<uint16_t>(p + 34 * c);
+        r.q[b] = load_unaligned<uint2>(p + 34 * c + 2 + 8 * o);
+    }
     template <typename P>
     static __device__ void load(Raw &r, P p, int o, int nvalid) {
 #pragma unroll
-        for (int b = 0; b < 8; ++b) {
-            const int c = nvalid == 8 ? b : min(b, nvalid - 1);
-            r.d[b] = load_unaligned<uint16_t>(p + 34 * c);
-            r.q[b] = load_unaligned<uint2>(p + 34 * c + 2 + 8 * o);
-        }
+        for (int b = 0; b < 8; ++b) load_block(r, p, o, nvalid, b);
     }
     template <bool MMA> static constexpr int mode() { return MMQ_BLOCK; }
     template <bool MMA> static __device__ uint64_t codes(const Raw &r, int b, int, const uint32_t *) { return u64(r.q[b]); }
@@ -75,14 +79,17 @@ template <> struct MmqW<Q4_0> {
         uint2 q[8];
         uint32_t d[8];
     };
+    static constexpr bool LAZY = true;  // independent blocks, as Q8_0
+    template <typename P>
+    static __device__ void load_block(Raw &r, P p, int o, int nvalid, int b) {
+        const int c = nvalid == 8 ? b : min(b, nvalid - 1);
+        r.d[b] = load_unaligned<uint16_t>(p + 18 * c);
+        r.q[b] = load_unaligned<uint2>(p + 18 * c + 2 + 8 * (o & 1));
+    }
     template <typename P>
     static __device__ void load(Raw &r, P p, int o, int nvalid) {
 #pragma unroll
-        for (int b = 0; b < 8; ++b) {
-            const int c = nvalid == 8 ? b : min(b, nvalid - 1);
-            r.d[b] = load_unaligned<uint16_t>(p + 18 * c);
-            r.q[b] = load_unaligned<uint2>(p + 18 * c + 2 + 8 * (o & 1));
-        }
+        for (int b = 0; b < 8; ++b) load_block(r, p, o, nvalid, b);
     }
     template <bool MMA> static constexpr int mode() { return MMQ_BLOCK; }
     template <bool MMA> static __device__ uint64_t codes(const Raw &r, int b, int o, const uint32_t *) {
@@ -257,6 +264,15 @@ template <> struct MmqW<IQ3_S> {
 
 // The MMQ kernel's view of a format: MmqW plus the lane's activation octet and the
 // 16-value half it holds (used by the split Q6_K MFMA), and a post-load fix-up hook.
+template <typename W, typename = void>
+struct LazyLoad {
+    static constexpr bool value = false;
+};
+template <typename W>
+struct LazyLoad<W, decltype(void(W::LAZY))> {
+    static constexpr bool value = W::LAZY;
+};
+
 template <int TYPE>
 struct MmqLoad : MmqW<TYPE> {
     static __device__ int act_pos(int g) { return 8 * g; }

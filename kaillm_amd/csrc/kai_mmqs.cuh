@@ -44,18 +44,26 @@ constexpr int mmqs_step_bytes() {  // one K step of 16 activation rows in LDS
 // `base`, the block epilogue, and the min terms. Batched (MMA) arithmetic of the format.
 // Each group of HALF blocks runs in phases: operand reads and codes, then the MFMAs, then
 // the epilogues, so every MFMA's latency is covered by the other blocks' work.
+// The weight fields come from the wave's transpose buffer row `wp` (the lane's row, octet
+// oct; nvalid blocks of the step inside the row): all at once, or per block for formats
+// whose blocks are independent (LAZY), which keeps them out of the registers until used.
 template <int TYPE>
-__device__ __forceinline__ void mmqs_step(typename MmqW<TYPE>::Raw &w, const uint8_t *base, v4f_t &acc, int col,
+__device__ __forceinline__ void mmqs_step(const lds_u8 *wp, int nvalid, const uint8_t *base, v4f_t &acc, int col,
                                           int oct, int aoct, const uint32_t *grid) {
     using W = MmqLoad<TYPE>;
     constexpr int MODE = W::template mode<true>();
+    constexpr bool LAZY = LazyLoad<MmqW<TYPE>>::value;
     // blocks per phase: their MFMA results, operands and scales are live at once
     constexpr int MT = 16, NT = W::NTERM, HALF = MODE == MMQ_BLOCK ? 4 : 2;
     constexpr int D8_OFF = MT * 8 * 32, TA_OFF = D8_OFF + MT * 8 * 4;
     const float *d8s = reinterpret_cast<const float *>(base + D8_OFF);
     const v4i_t zero = {0, 0, 0, 0};
     const bool first = W::first_half(oct);
-    W::fix(w);
+    typename W::Raw w;
+    if constexpr (!LAZY) {
+        W::load(w, wp, oct, nvalid);
+        W::fix(w);
+    }
 #pragma unroll
     for (int h = 0; h < 8; h += HALF) {
         long aq[HALF], bq[HALF];
@@ -63,6 +71,7 @@ __device__ __forceinline__ void mmqs_step(typename MmqW<TYPE>::Raw &w, const uin
 #pragma unroll
         for (int u = 0; u < HALF; ++u) {
             const int b = h + u;
+            if constexpr (LAZY) W::load_block(w, wp, oct, nvalid, b);
             aq[u] = *reinterpret_cast<const long *>(base + (b * MT + col) * 32 + 8 * (aoct ^ ((col >> 2) & 3)));
             dv[u] = *reinterpret_cast<const float4 *>(d8s + b * MT + 4 * oct);
             bq[u] = static_cast<long>(W::template codes<true>(w, b, oct, grid));
@@ -265,12 +274,13 @@ __global__ __launch_bounds__(WAVES * WAVE) void mmqs_kernel(
     const int buf_off = mmqs_positions(split.chunk) * BUF;  // the transpose buffers follow the largest chunk
     lds_u8 *tb = (lds_u8 *)kai_mmqs_lds + buf_off + wave * (16 * S::SBP + 16);
     // piece q of row set r is this wave's index minus that of the wave holding the set's
-    // first step; it goes to partial [chunk][row set][q] as [16 columns][16 rows] fp32, one
-    // 16-byte store per lane
+    // first step; it goes to partial [chunk][row set][q] as [16 activation rows][16 columns]
+    // fp32 (rows past m are zero), so that the reduction reads and writes whole rows
     auto store = [&](const v4f_t &acc, int r) {
         const int q = w - (r * sce) / run;
-        float *p = partial + (((int64_t(chunk_id) * rowsets + r) * split.qmax + q) * 16 + col) * 16 + 4 * oct;
-        *reinterpret_cast<float4 *>(p) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        float *p = partial + (((int64_t(chunk_id) * rowsets + r) * split.qmax + q) * 16 + 4 * oct) * 16 + col;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p[16 * i] = acc[i];
     };
     auto loop = [&](auto careful_tag) {
 #pragma unroll 1
@@ -289,9 +299,8 @@ __global__ __launch_bounds__(WAVES * WAVE) void mmqs_kernel(
                         else
                             store16(tb + uoff[i], sl.v[i]);
                     }
-                    typename W::Raw raw;
-                    W::load(raw, tb + col * S::SBP, oct, min(8, nb - 8 * (s0 + min(j + d, sc - 1))));
-                    mmqs_step<TYPE>(raw, kai_mmqs_lds + (j + d) * BUF, acc, col, oct, aoct, grid_lds);
+                    mmqs_step<TYPE>(tb + col * S::SBP, min(8, nb - 8 * (s0 + min(j + d, sc - 1))),
+                                    kai_mmqs_lds + (j + d) * BUF, acc, col, oct, aoct, grid_lds);
                     wload(wr[d], careful_tag);
                     // keep the refill here and each step's work in its own section: without
                     // these fences the loads are sunk to their use and the next slot's decode
@@ -304,12 +313,20 @@ __global__ __launch_bounds__(WAVES * WAVE) void mmqs_kernel(
             pa = pb;
         }
     };
-    if (careful) loop(std::true_type{});
-    else loop(std::false_type{});
+    // Q8_0 and Q4_0 (whose raw fields are many small pieces) run every wave on the clamped
+    // copy: two copies of their loop do not fit the 128 registers without spilling
+    if constexpr (LazyLoad<MmqW<TYPE>>::value) {
+        loop(std::true_type{});
+    } else {
+        if (careful) loop(std::true_type{});
+        else loop(std::false_type{});
+    }
 }
 
 // out[row][c] = inverse[row] * sum over chunks, then pieces (in order), of the partial sums
-// of c's row set.
+// of c's row set. (Combining the pieces in the GEMM itself, by the last wave to finish a row
+// set, needs an agent-scope release and acquire per wave: on MI355X those write back and
+// invalidate the XCD's L2 and made the GEMM six times slower.)
 static __global__ __launch_bounds__(256) void mmqs_reduce_kernel(const float *__restrict__ partial, MmqsSplit split,
                                                                   int steps, int m, int n,
                                                                   const float *__restrict__ inverse,
@@ -322,9 +339,9 @@ static __global__ __launch_bounds__(256) void mmqs_reduce_kernel(const float *__
     float s = 0.0f;
     for (int ch = 0; ch < split.chunks; ++ch) {
         const int sc = mmqs_chunk_steps(split, steps, ch), sce = mmqs_positions(sc), run = mmqs_run(split, rowsets, sc);
-        const int first = (r * sce) / run, last = (r * sce + sce - 1) / run;
-        const float *p = partial + ((int64_t(ch) * rowsets + r) * split.qmax * 16 + c % 16) * 16 + row;
-        for (int q = 0; q <= last - first; ++q) s += p[q * 256];
+        const int np = (r * sce + sce - 1) / run - (r * sce) / run + 1;
+        const float *p = partial + ((int64_t(ch) * rowsets + r) * split.qmax * 16 + row) * 16 + c % 16;
+        for (int q = 0; q < np; ++q) s += p[q * 256];
     }
     const float v = s * inverse[row];
     const int64_t idx = int64_t(row) * stride_dst + c;
