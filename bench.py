@@ -70,8 +70,10 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--kernel-sample", action="store_true",
-                   help="counter-collection run: a 256 MiB device copy (calibration) and the dominant "
-                        "GEMV on each weight copy, eager launches only")
+                   help="counter-collection run: a 256 MiB device copy (calibration) and the decode "
+                        "kernels of one C3 matrix on each weight copy, eager launches only")
+    p.add_argument("--sample-matrix", default="gate_up", choices=[c[0] for c in C3],
+                   help="the C3 matrix of --kernel-sample")
     return p.parse_args()
 
 
@@ -192,7 +194,7 @@ def main():
     torch.cuda.set_device(dev)
     batches = [int(b) for b in args.batches.split(",")]
     if args.kernel_sample:
-        kernel_sample(lib, dev, batches)
+        kernel_sample(lib, dev, batches, args.sample_matrix)
         return
     chosen = set(("C1,C2,C3,C4,C5" if args.legs == "all" else "" if args.legs == "none" else args.legs).split(","))
 
@@ -304,18 +306,18 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def kernel_sample(lib, dev, batches):
+def kernel_sample(lib, dev, batches, matrix="gate_up"):
     """Eager launches for rocprofv3 --pmc runs: FETCH_SIZE / WRITE_SIZE of a plain copy of
-    known size (the calibration) next to those of the Q4_K gate/up decode kernel per batch."""
+    known size (the calibration) next to those of one C3 matrix's decode kernels per batch."""
     import torch
 
     from kaillm_amd import native
     from kaillm_amd.formats import quantize
 
-    n, k = 34816, 5120
+    _, qtype, n, k = next(c for c in C3 if c[0] == matrix)
     g = torch.Generator(device=dev).manual_seed(1000)
     w32 = torch.randn((n, k), generator=g, device=dev, dtype=torch.float32).mul_(0.02).cpu().numpy()
-    packed = torch.from_numpy(quantize(w32, Q4_K)).to(dev)
+    packed = torch.from_numpy(quantize(w32, qtype)).to(dev)
     copies = [packed] + [packed.clone() for _ in range(MIN_COPIES - 1)]
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
@@ -325,12 +327,12 @@ def kernel_sample(lib, dev, batches):
     out = torch.empty((max(batches), n), dtype=torch.float32, device=dev)
     act = torch.empty(lib.kai_fused_activation_bytes(max(batches), k, 0), dtype=torch.uint8, device=dev)
     s = torch.cuda.current_stream().cuda_stream
-    types, rows = (ctypes.c_int * 1)(Q4_K), (ctypes.c_int64 * 1)(n)
+    types, rows = (ctypes.c_int * 1)(qtype), (ctypes.c_int64 * 1)(n)
     for m in batches:
         if m <= 8:
             native.check(lib, lib.kai_fused_prepare(x.data_ptr(), 2, m, k, k, act.data_ptr(), 0, s))
             for c in copies:
-                native.check(lib, lib.kai_fused_mmvq(c.data_ptr(), Q4_K, n, k, m, act.data_ptr(), 0,
+                native.check(lib, lib.kai_fused_mmvq(c.data_ptr(), qtype, n, k, m, act.data_ptr(), 0,
                                                      out.data_ptr(), 0, n, s))
         else:
             size = lib.kai_fused_mmq_workspace(0, types, rows, 1, k, m, 1)
@@ -340,7 +342,7 @@ def kernel_sample(lib, dev, batches):
                 native.check(lib, lib.kai_fused_mmq_run(ptrs, types, rows, 1, x.data_ptr(), 2, k, k, m,
                                                         out.data_ptr(), 0, 0, scratch.data_ptr(), size, 0, s))
     torch.cuda.synchronize()
-    print(f"[bench] kernel sample: 3 copies of {src.numel()} bytes, Q4_K {n}x{k} x{MIN_COPIES} "
+    print(f"[bench] kernel sample: 3 copies of {src.numel()} bytes, {matrix} {NAMES[qtype]} {n}x{k} x{MIN_COPIES} "
           f"at batch {batches}", flush=True)
 
 
