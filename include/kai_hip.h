@@ -81,6 +81,39 @@ int kai_fused_norm_prepare(const void *x, int x_dtype, int64_t stride_x, const v
 int kai_dequantize(const void *weight, int type, int64_t rows, int64_t cols, void *out, int out_dtype,
                    uintptr_t stream);
 
+/* The legacy _C_gguf ops. The reference binds them as torch ops (schema
+ * csrc/torch_bindings.cpp:22-53) with no C entry points; these are their C form.
+ *
+ * kai_ggml_quantize_q8_1: the legacy Q8_1 activation of x [m, k] (row stride stride_x) in
+ * kai_fused_prepare's single-pass layout (kai_fused_activation_bytes(m, k, 0) bytes): per 32
+ * values with no row normalisation, d = max|x| / 127, q = max|x| == 0 ? 0 : roundf(x / d),
+ * ds = (half(d), half(sum x)) with sum x grouped as a 32-lane xor butterfly (masks 16, 8, 4,
+ * 2, 1), inverse[row] = 1. Replaces quantize_row_q8_1_cuda (csrc/gguf/gguf_kernel.cu:32-85),
+ * which spaces its rows K padded to 512 with zero blocks that no product reads. */
+int kai_ggml_quantize_q8_1(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, void *activation,
+                           uintptr_t stream);
+
+/* Scratch bytes of one kai_ggml_mul_mat_vec_a8 (batched = 0) or kai_ggml_mul_mat_a8
+ * (batched = 1) call; 0 with a message when the call would be rejected. */
+size_t kai_ggml_a8_workspace(int type, int64_t row, int64_t k, int64_t vecs, int batched);
+
+/* y [vecs, row] (dense; F32, or BF16 when y_bf16) = x [vecs, k] @ W^T over the legacy
+ * activation (kai_ggml_quantize_q8_1's arithmetic), W the GGUF wire bytes [row, k / qk *
+ * block_bytes]; k <= 32768.
+ * kai_ggml_mul_mat_vec_a8 takes the legacy MMVQ block dots (Q4_0's offset from the stored
+ * half(sum x); Q4_K and Q2_K mins from d8 * sum q). Replaces ggml_mul_mat_vec_a8
+ * (csrc/gguf/gguf_kernel.cu:104-218).
+ * kai_ggml_mul_mat_a8 takes the legacy MMQ block dots, which differ only in Q4_K's min term
+ * (the stored half(sum x)); every type but IQ3_S (the reference has no such kernel), and on
+ * Q4_K, Q8_0 and Q6_K a multiple of four rows. Replaces ggml_mul_mat_a8
+ * (csrc/gguf/gguf_kernel.cu:220-290). */
+int kai_ggml_mul_mat_vec_a8(const void *weight, int type, int64_t row, const void *x, int x_dtype, int64_t vecs,
+                            int64_t k, int64_t stride_x, void *y, int y_bf16, void *scratch, size_t scratch_bytes,
+                            uintptr_t stream);
+int kai_ggml_mul_mat_a8(const void *weight, int type, int64_t row, const void *x, int x_dtype, int64_t vecs,
+                        int64_t k, int64_t stride_x, void *y, int y_bf16, void *scratch, size_t scratch_bytes,
+                        uintptr_t stream);
+
 /* Copy a GGUF tensor's rows from the model file at `path` into device memory, bytes
  * unchanged: the tensor starts at file_offset and holds src_rows rows of row_bytes. dst row r
  * (r < rows) receives source row row_order[r] (row_order NULL: row r); with block_order,

@@ -113,6 +113,74 @@ void run_mmq_group(const void *const *weights, const int *types, const int64_t *
     }
 }
 
+// kai_fused_mmvq's product over a single-pass (or two-pass) activation of m <= 8 rows: the
+// v_dot4 GEMV, or the paired int8 tile above gemv_max_rows(type) rows or when the rows do
+// not fit the GEMV's LDS staging.
+void run_decode(int type, const void *weight, int64_t n, int64_t k, int64_t m, const kai::ActLayout &l, void *dst,
+                bool dst_bf16, int64_t stride_dst, hipStream_t s) {
+    if (!l.y2 && (m > kai::gemv_max_rows(type) || !kai::gemv_one_launch(m, k, 0)) && k % 256 == 0)
+        kai::launch_mmq(type, weight, n, k, m, l.y1, l.inverse, dst, dst_bf16, stride_dst, s);
+    else
+        kai::launch_mmvq(type, weight, n, k, m, l.y1, l.y2, l.inverse, dst, dst_bf16, stride_dst, s);
+}
+
+// The legacy ops (csrc/gguf/gguf_kernel.cu:104-290). ggml_mul_mat_a8 on Q4_K, Q8_0 and Q6_K
+// runs the batched kernels over the legacy D4 / DS4 planes with exact weight products (Q4_K's
+// min term then takes the stored half(sum x) and dmin * m in fp32, vecdotq.cuh:353-377). ggml_mul_mat_vec_a8, and ggml_mul_mat_a8 on
+// Q4_0 and Q2_K, whose legacy MMQ block dots are the MMVQ ones (vecdotq.cuh:46-66, :204-261),
+// run the decode kernels over the legacy Q8_1 activation, 8 rows per launch.
+bool legacy_on_planes(int type, bool batched) {
+    return batched && (type == kai::Q4_K || type == kai::Q8_0 || type == kai::Q6_K);
+}
+
+void legacy_check(int type, int64_t n, int64_t k, int64_t m, bool batched) {
+    if (!kai::weight_type_supported(type)) throw kai::Error("Unsupported GGML weight type");
+    if (batched && type == kai::IQ3_S)
+        throw kai::Error("ggml_mul_mat_a8 has no IQ3_S kernel (csrc/gguf/gguf_kernel.cu:229-288)");
+    if (!shape_ok(type, n, k, 1, 1) || m < 1 || m > INT_MAX) throw kai::Error("Invalid legacy product shape");
+    if (legacy_on_planes(type, batched) && n % 4) throw kai::Error("ggml_mul_mat_a8 takes a multiple of four rows");
+}
+
+size_t legacy_scratch(int type, int64_t n, int64_t k, int64_t m, bool batched) {
+    if (legacy_on_planes(type, batched)) return mmq_scratch(&type, &n, 1, k, m).total;
+    return activation_bytes(m, k, 0);
+}
+
+int legacy_mul_mat(bool batched, const void *weight, int type, int64_t row, const void *x, int x_dtype, int64_t vecs,
+                   int64_t k, int64_t stride_x, void *y, int y_bf16, void *scratch, size_t scratch_bytes,
+                   uintptr_t stream) {
+    return entry([&] {
+        legacy_check(type, row, k, vecs, batched);
+        if (!weight || !x || !y || !scratch || stride_x < k) throw kai::Error("Invalid legacy product arguments");
+        if (scratch_bytes < legacy_scratch(type, row, k, vecs, batched))
+            throw kai::Error("Scratch is smaller than kai_ggml_a8_workspace");
+        const hipStream_t s = stream_of(stream);
+        char *base = static_cast<char *>(scratch);
+        if (legacy_on_planes(type, batched)) {
+            const MmqScratch plan = mmq_scratch(&type, &row, 1, k, vecs);
+            const int layout = kai::mmq_layout(type);
+            float *inverse = reinterpret_cast<float *>(base + plan.inverse);
+            uint8_t *plane = reinterpret_cast<uint8_t *>(base + plan.plane[layout]);
+            kai::MmqPlanes p{layout == kai::MMQ_D4 ? plane : nullptr, layout == kai::MMQ_DS4 ? plane : nullptr, nullptr,
+                             inverse, vecs <= kai::MMQS_MAX_ROWS, true};
+            kai::launch_prepare_mmq(x, x_dtype, vecs, k, stride_x, p, s);
+            kai::launch_mmq_planes(type, weight, row, k, vecs, plane, inverse,
+                                   reinterpret_cast<float *>(base + plan.partial), plan.partial_bytes, y, y_bf16 != 0,
+                                   row, s, true);
+            return;
+        }
+        const kai::ActLayout l = activation_layout(scratch, vecs, k, 0);
+        kai::launch_prepare_legacy(x, x_dtype, vecs, k, stride_x, l, s);
+        const int64_t nb = k / kai::QK8_1;
+        const size_t elem = y_bf16 ? 2 : 4;
+        for (int64_t j0 = 0; j0 < vecs; j0 += MAX_FUSED_ROWS) {
+            const kai::ActLayout c{l.y1 + j0 * nb, nullptr, l.inverse + j0};
+            run_decode(type, weight, row, k, std::min<int64_t>(MAX_FUSED_ROWS, vecs - j0), c,
+                       static_cast<char *>(y) + size_t(j0) * size_t(row) * elem, y_bf16 != 0, row, s);
+        }
+    });
+}
+
 }  // namespace
 
 namespace kai {
@@ -223,13 +291,44 @@ extern "C" int kai_fused_mmvq(const void *weight, int type, int64_t n, int64_t k
         if (!weight || !activation || !dst || !shape_ok(type, n, k, m, MAX_FUSED_ROWS) || stride_dst < n ||
             stride_dst > INT_MAX)
             throw kai::Error("Invalid fused MMVQ arguments");
-        const kai::ActLayout l = activation_layout(const_cast<void *>(activation), m, k, two_pass);
-        if (!two_pass && (m > kai::gemv_max_rows(type) || !kai::gemv_one_launch(m, k, 0)) && k % 256 == 0)
-            kai::launch_mmq(type, weight, n, k, m, l.y1, l.inverse, dst, dst_bf16 != 0, stride_dst, stream_of(stream));
-        else
-            kai::launch_mmvq(type, weight, n, k, m, l.y1, l.y2, l.inverse, dst, dst_bf16 != 0, stride_dst,
-                             stream_of(stream));
+        run_decode(type, weight, n, k, m, activation_layout(const_cast<void *>(activation), m, k, two_pass), dst,
+                   dst_bf16 != 0, stride_dst, stream_of(stream));
     });
+}
+
+extern "C" int kai_ggml_quantize_q8_1(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x,
+                                      void *activation, uintptr_t stream) {
+    return entry([&] {
+        if (!x || !activation || m < 1 || m > INT_MAX || k <= 0 || k % kai::QK8_1 || stride_x < k)
+            throw kai::Error("Invalid legacy activation arguments");
+        kai::launch_prepare_legacy(x, x_dtype, m, k, stride_x, activation_layout(activation, m, k, 0),
+                                   stream_of(stream));
+    });
+}
+
+extern "C" size_t kai_ggml_a8_workspace(int type, int64_t row, int64_t k, int64_t vecs, int batched) {
+    try {
+        last_error.clear();
+        legacy_check(type, row, k, vecs, batched != 0);
+        return legacy_scratch(type, row, k, vecs, batched != 0);
+    } catch (const std::exception &error) {
+        last_error = error.what();
+        return 0;
+    }
+}
+
+extern "C" int kai_ggml_mul_mat_vec_a8(const void *weight, int type, int64_t row, const void *x, int x_dtype,
+                                       int64_t vecs, int64_t k, int64_t stride_x, void *y, int y_bf16, void *scratch,
+                                       size_t scratch_bytes, uintptr_t stream) {
+    return legacy_mul_mat(false, weight, type, row, x, x_dtype, vecs, k, stride_x, y, y_bf16, scratch, scratch_bytes,
+                          stream);
+}
+
+extern "C" int kai_ggml_mul_mat_a8(const void *weight, int type, int64_t row, const void *x, int x_dtype,
+                                   int64_t vecs, int64_t k, int64_t stride_x, void *y, int y_bf16, void *scratch,
+                                   size_t scratch_bytes, uintptr_t stream) {
+    return legacy_mul_mat(true, weight, type, row, x, x_dtype, vecs, k, stride_x, y, y_bf16, scratch, scratch_bytes,
+                          stream);
 }
 
 extern "C" size_t kai_fused_mmq_workspace(int device, const int *types, const int64_t *rows, int count, int64_t k,

@@ -77,6 +77,10 @@ void launch_prepare(const void *x, int x_dtype, int64_t m, int64_t k, int64_t st
                     hipStream_t stream);
 // Fused producers of the single-pass activation (kai_prepare.hip): x[..., view], silu(gate)
 // * up from a merged [gate | up] row, and Gemma RMSNorm (+ residual) writing bf16 y.
+// The legacy _C_gguf ops' Q8_1 activation (no row normalisation, ds = (half(d), half(sum x)),
+// inverse 1) into the single-pass layout.
+void launch_prepare_legacy(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const ActLayout &out,
+                           hipStream_t stream);
 void launch_prepare_view(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, int64_t a, int64_t b,
                          int64_t s, const ActLayout &out, hipStream_t stream);
 void launch_prepare_swiglu(const void *gate_up, int dtype, int64_t m, int64_t k, int64_t stride, const ActLayout &out,
@@ -112,10 +116,11 @@ void launch_mmq(int type, const void *weight, int64_t n, int64_t k, int64_t m, c
 // is a whole number of the type's blocks): up to MMQS_MAX_ROWS rows on the small-M GEMM
 // (kai_mmqs.cuh) reading the layout's small-M image, which may need
 // mmq_partial_bytes(type, m, n, k) of scratch for K-chunk partial sums; more rows on the
-// tiled int8 GEMM (kai_mmq.cuh) reading the plane.
+// tiled int8 GEMM (kai_mmq.cuh) reading the plane. exact: the legacy MMQ's weight arithmetic
+// (d * sc and dmin * m in fp32; differs from GGML MMQ's fp16 roundings for Q4_K only).
 void launch_mmq_planes(int type, const void *weight, int64_t n, int64_t k, int64_t m, const uint8_t *plane,
                        const float *inverse, float *partial, size_t partial_bytes, void *dst, bool dst_bf16,
-                       int64_t stride_dst, hipStream_t stream);
+                       int64_t stride_dst, hipStream_t stream, bool exact = false);
 size_t mmq_partial_bytes(int type, int64_t m, int64_t n, int64_t k);
 
 // Batched path (kai_fused_mmq_run): activation planes of GGML's MMQ quantisation, one per
@@ -151,7 +156,8 @@ inline size_t mmqs_image_bytes(int layout, int64_t k) { return size_t(mmqs_steps
 struct MmqPlanes {
     uint8_t *d4, *ds4, *d2s6;  // null when no matrix of the group reads that layout
     float *inverse;
-    bool image;  // small-M images (m <= MMQS_MAX_ROWS) instead of planes
+    bool image;          // small-M images (m <= MMQS_MAX_ROWS) instead of planes
+    bool legacy = false;  // the legacy ops' quantisation (launch_prepare_legacy's), D4 / DS4 only
 };
 void launch_prepare_mmq(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const MmqPlanes &planes,
                         hipStream_t stream);

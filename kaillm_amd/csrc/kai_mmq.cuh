@@ -106,13 +106,17 @@ constexpr size_t mmq_lds_bytes() {
 // PAIR: up to 8 rows of decode Q8_1 blocks (act: block_q8_1 [m][k/32], k % 256 == 0);
 // otherwise the batched path's plane of the type's layout (act: uint8 plane), any k that is
 // a whole number of blocks (a short last step reads zero activations).
-template <int TYPE, int TM, int TN, int KS, int DEPTH, bool PAIR>
+// EXACT (planes only): the decode path's exact weight products in place of GGML MMQ's
+// fp16-rounded ones; the legacy MMQ keeps d * sc and dmin * m in fp32 (vecdotq.cuh:353-377).
+template <int TYPE, int TM, int TN, int KS, int DEPTH, bool PAIR, bool EXACT = false>
 __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
     const uint8_t *__restrict__ weight, int64_t row_bytes, int n, int k, const void *__restrict__ act,
     int m, const float *__restrict__ inverse, void *__restrict__ dst, int64_t stride_dst, int dst_bf16) {
     using W = MmqLoad<TYPE>;
     static_assert(!PAIR || TM == 1, "paired blocks use one tile of 8 activation rows");
-    constexpr int MODE = W::template mode<!PAIR>();  // decode (paired) or batched arithmetic
+    static_assert(!(PAIR && EXACT), "the paired tile's arithmetic is exact already");
+    constexpr bool BATCHED = !PAIR && !EXACT;  // GGML MMQ's weight arithmetic
+    constexpr int MODE = W::template mode<BATCHED>();  // decode (paired) or batched arithmetic
     constexpr int MT = PAIR ? 8 : 16 * TM, RG = 4 / KS, NT = W::NTERM;
     constexpr int BUF = mmq_buf_bytes<TYPE, TM>();
     constexpr int D8_OFF = MT * 8 * 32, TA_OFF = D8_OFF + MT * 8 * 4;
@@ -278,7 +282,7 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
             int sl[TN], sh[TN];
 #pragma unroll
             for (int t = 0; t < TN; ++t) {
-                const uint64_t c = W::template codes<true>(w[t], b, oct, grid_lds);
+                const uint64_t c = W::template codes<BATCHED>(w[t], b, oct, grid_lds);
                 if constexpr (MODE != MMQ_BLOCK) {
                     const bool first = W::first_half(oct);
                     bq[t] = first ? c : 0ull;
@@ -294,7 +298,7 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
                     fl[t] = W::fscale(w[t], 2 * b);
                     fh[t] = W::fscale(w[t], 2 * b + 1);
                 } else {
-                    sa[t] = W::template scale<true>(w[t], b);
+                    sa[t] = W::template scale<BATCHED>(w[t], b);
                 }
             }
 #pragma unroll
@@ -332,7 +336,7 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
             for (int j = 0; j < NT / 4; ++j) {
                 float bt[TN];
 #pragma unroll
-                for (int t = 0; t < TN; ++t) bt[t] = W::template term<!PAIR>(w[t], j, oct);
+                for (int t = 0; t < TN; ++t) bt[t] = W::template term<BATCHED>(w[t], j, oct);
 #pragma unroll
                 for (int a = 0; a < TM; ++a) {
                     // paired: the terms go to D rows 0-7 (activation rows 0-7), A rows 8-15 zero
@@ -425,7 +429,7 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
     }
 }
 
-template <int TYPE, int TM, int TN, int KS, bool PAIR = false>
+template <int TYPE, int TM, int TN, int KS, bool PAIR = false, bool EXACT = false>
 static void launch_mmq_tile(const void *weight, int64_t n, int64_t k, const void *act, int64_t m,
                             const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
     constexpr int MT = PAIR ? 8 : 16 * TM, ROWS = 16 * TN * (4 / KS);
@@ -437,7 +441,7 @@ static void launch_mmq_tile(const void *weight, int64_t n, int64_t k, const void
     // three / two / one steps; at 32-80 rows one against two steps, Q4_0 -5..-13 %, Q6_K
     // and Q2_K unchanged.
     constexpr int DEPTH = 1;
-    auto kernel = mmq_kernel<TYPE, TM, TN, KS, DEPTH, PAIR>;
+    auto kernel = mmq_kernel<TYPE, TM, TN, KS, DEPTH, PAIR, EXACT>;
     static DeviceFlags lds_raised;
     raise_dynamic_lds(reinterpret_cast<const void *>(kernel), lds, lds_raised, "Cannot raise the MMQ dynamic LDS limit");
     const dim3 grid(static_cast<unsigned>((n + ROWS - 1) / ROWS), static_cast<unsigned>((m + MT - 1) / MT));
@@ -456,8 +460,8 @@ constexpr bool mmq_allowed(int tm, int ks) { return ks == 1 || (ks == 2 && tm <=
 
 // PLANES: act is the batched path's plane of the type's layout (kai_fused_mmq_run, any m,
 // k a whole number of blocks); otherwise decode Q8_1 blocks, up to 8 rows on the paired
-// tile (kai_fused_mmvq), k % 256 == 0.
-template <int TYPE, bool PLANES>
+// tile (kai_fused_mmvq), k % 256 == 0. EXACT: planes with mmq_kernel's exact weight products.
+template <int TYPE, bool PLANES, bool EXACT = false>
 void launch_mmq_type(const void *weight, int64_t n, int64_t k, int64_t m, const void *act, const float *inverse,
                      void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
     if (!PLANES && k % MMQ_STEP) throw Error("MMQ on decode activations needs k to be a multiple of 256");
@@ -496,7 +500,8 @@ void launch_mmq_type(const void *weight, int64_t n, int64_t k, int64_t m, const 
 #define KAI_C(TM, TN, KS) \
     case TM * 100 + TN * 10 + KS: \
         if constexpr (TN == 1 || wide) \
-            launch_mmq_tile<TYPE, TM, TN, KS>(weight, n, k, act, m, inverse, dst, dst_bf16, stride_dst, stream); \
+            launch_mmq_tile<TYPE, TM, TN, KS, false, EXACT>(weight, n, k, act, m, inverse, dst, dst_bf16, stride_dst, \
+                                                           stream); \
         break;
             KAI_C(1, 2, 1) KAI_C(1, 1, 1) KAI_C(1, 2, 2) KAI_C(1, 1, 2) KAI_C(1, 1, 4)
             KAI_C(2, 2, 1) KAI_C(2, 1, 1) KAI_C(2, 2, 2) KAI_C(2, 1, 2)

@@ -3,6 +3,21 @@
 
 namespace kai {
 
+// The kernels are compiled in the per-type files; this file only dispatches.
+#define KAI_EXTERN(T) \
+    extern template void launch_mmq_type<T, false>(const void *, int64_t, int64_t, int64_t, const void *, \
+                                                   const float *, void *, bool, int64_t, hipStream_t); \
+    extern template void launch_mmq_type<T, true>(const void *, int64_t, int64_t, int64_t, const void *, \
+                                                  const float *, void *, bool, int64_t, hipStream_t); \
+    extern template void launch_mmqs<T>(const void *, int64_t, int64_t, int64_t, const uint8_t *, const float *, \
+                                        float *, size_t, void *, bool, int64_t, hipStream_t);
+KAI_EXTERN(Q8_0) KAI_EXTERN(Q4_0) KAI_EXTERN(Q4_K) KAI_EXTERN(Q6_K) KAI_EXTERN(Q2_K) KAI_EXTERN(IQ3_S)
+#undef KAI_EXTERN
+extern template void launch_mmq_type<Q4_K, true, true>(const void *, int64_t, int64_t, int64_t, const void *,
+                                                       const float *, void *, bool, int64_t, hipStream_t);
+extern template void launch_mmqs<Q4_K, true>(const void *, int64_t, int64_t, int64_t, const uint8_t *, const float *,
+                                             float *, size_t, void *, bool, int64_t, hipStream_t);
+
 template <bool PLANES>
 static void dispatch(int type, const void *weight, int64_t n, int64_t k, int64_t m, const void *act,
                      const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
@@ -22,7 +37,16 @@ void launch_mmq(int type, const void *weight, int64_t n, int64_t k, int64_t m, c
 
 void launch_mmq_planes(int type, const void *weight, int64_t n, int64_t k, int64_t m, const uint8_t *plane,
                        const float *inverse, float *partial, size_t partial_bytes, void *dst, bool dst_bf16,
-                       int64_t stride_dst, hipStream_t stream) {
+                       int64_t stride_dst, hipStream_t stream, bool exact) {
+    if (exact && type == Q4_K) {  // the only format whose batched weight arithmetic rounds
+        if (m <= MMQS_MAX_ROWS)
+            launch_mmqs<Q4_K, true>(weight, n, k, m, plane, inverse, partial, partial_bytes, dst, dst_bf16, stride_dst,
+                                    stream);
+        else
+            launch_mmq_type<Q4_K, true, true>(weight, n, k, m, plane, inverse, dst, dst_bf16, stride_dst, stream);
+        return;
+    }
+    if (exact && type != Q8_0 && type != Q6_K) throw Error("Exact batched arithmetic covers Q4_K, Q8_0 and Q6_K");
     if (m <= MMQS_MAX_ROWS) {
         switch (type) {
 #define KAI_T(T) \

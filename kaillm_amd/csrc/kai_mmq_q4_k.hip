@@ -8,4 +8,9 @@ template void launch_mmq_type<Q4_K, true>(const void *, int64_t, int64_t, int64_
                                       bool, int64_t, hipStream_t);
 template void launch_mmqs<Q4_K>(const void *, int64_t, int64_t, int64_t, const uint8_t *, const float *, float *,
                              size_t, void *, bool, int64_t, hipStream_t);
+// the legacy ops' exact weight products
+template void launch_mmq_type<Q4_K, true, true>(const void *, int64_t, int64_t, int64_t, const void *, const float *,
+                                                void *, bool, int64_t, hipStream_t);
+template void launch_mmqs<Q4_K, true>(const void *, int64_t, int64_t, int64_t, const uint8_t *, const float *, float *,
+                                      size_t, void *, bool, int64_t, hipStream_t);
 }  // namespace kai

@@ -47,11 +47,13 @@ constexpr int mmqs_step_bytes() {  // one K step of 16 activation rows in LDS
 // The weight fields come from the wave's transpose buffer row `wp` (the lane's row, octet
 // oct; nvalid blocks of the step inside the row): all at once, or per block for formats
 // whose blocks are independent (LAZY), which keeps them out of the registers until used.
-template <int TYPE>
+// EXACT: the exact weight products of mmq_kernel's EXACT form (the legacy MMQ's arithmetic).
+template <int TYPE, bool EXACT>
 __device__ __forceinline__ void mmqs_step(const lds_u8 *wp, int nvalid, const uint8_t *base, v4f_t &acc, int col,
                                           int oct, int aoct, const uint32_t *grid) {
     using W = MmqLoad<TYPE>;
-    constexpr int MODE = W::template mode<true>();
+    constexpr bool BATCHED = !EXACT;
+    constexpr int MODE = W::template mode<BATCHED>();
     constexpr bool LAZY = LazyLoad<MmqW<TYPE>>::value;
     // blocks per phase: their MFMA results, operands and scales are live at once
     constexpr int MT = 16, NT = W::NTERM, HALF = MODE == MMQ_BLOCK ? 4 : 2;
@@ -74,7 +76,7 @@ __device__ __forceinline__ void mmqs_step(const lds_u8 *wp, int nvalid, const ui
             if constexpr (LAZY) W::load_block(w, wp, oct, nvalid, b);
             aq[u] = *reinterpret_cast<const long *>(base + (b * MT + col) * 32 + 8 * (aoct ^ ((col >> 2) & 3)));
             dv[u] = *reinterpret_cast<const float4 *>(d8s + b * MT + 4 * oct);
-            bq[u] = static_cast<long>(W::template codes<true>(w, b, oct, grid));
+            bq[u] = static_cast<long>(W::template codes<BATCHED>(w, b, oct, grid));
         }
         v4i_t r1[HALF], r2[HALF];
 #pragma unroll
@@ -91,11 +93,11 @@ __device__ __forceinline__ void mmqs_step(const lds_u8 *wp, int nvalid, const ui
             const int b = h + u;
             const float d8[4] = {dv[u].x, dv[u].y, dv[u].z, dv[u].w};
             if constexpr (MODE == MMQ_BLOCK) {
-                const float sa = W::template scale<true>(w, b);
+                const float sa = W::template scale<BATCHED>(w, b);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[i] = fmaf(d8[i] * sa, static_cast<float>(r1[u][i]), acc[i]);
             } else if constexpr (MODE == MMQ_ISPLIT) {
-                const float sa = W::template scale<true>(w, b);
+                const float sa = W::template scale<BATCHED>(w, b);
                 const int sl = W::iscale(w, 2 * b), sh = W::iscale(w, 2 * b + 1);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -117,7 +119,7 @@ __device__ __forceinline__ void mmqs_step(const lds_u8 *wp, int nvalid, const ui
         const float *ta = reinterpret_cast<const float *>(base + TA_OFF);
 #pragma unroll
         for (int j = 0; j < NT / 4; ++j)
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ta[(4 * j + oct) * MT + col], W::template term<true>(w, j, oct),
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ta[(4 * j + oct) * MT + col], W::template term<BATCHED>(w, j, oct),
                                                       acc, 0, 0, 0);
     }
 }
@@ -155,7 +157,7 @@ __host__ __device__ inline int mmqs_run(const MmqsSplit &p, int rowsets, int sc)
 }
 
 // grid: chunks * wgs workgroups of WAVES waves; workgroup b works on chunk b / wgs.
-template <int TYPE, int DEPTH, int WAVES>
+template <int TYPE, int DEPTH, int WAVES, bool EXACT = false>
 __global__ __launch_bounds__(WAVES * WAVE) void mmqs_kernel(
     const uint8_t *weight, int64_t row_bytes, int n, int k, const uint8_t *__restrict__ image, int m,
     const float *__restrict__ inverse, MmqsSplit split, float *__restrict__ partial, void *__restrict__ dst,
@@ -299,7 +301,7 @@ __global__ __launch_bounds__(WAVES * WAVE) void mmqs_kernel(
                         else
                             store16(tb + uoff[i], sl.v[i]);
                     }
-                    mmqs_step<TYPE>(tb + col * S::SBP, min(8, nb - 8 * (s0 + min(j + d, sc - 1))),
+                    mmqs_step<TYPE, EXACT>(tb + col * S::SBP, min(8, nb - 8 * (s0 + min(j + d, sc - 1))),
                                     kai_mmqs_lds + (j + d) * BUF, acc, col, oct, aoct, grid_lds);
                     wload(wr[d], careful_tag);
                     // keep the refill here and each step's work in its own section: without
@@ -391,8 +393,9 @@ inline size_t mmqs_partial_bytes(int64_t m, int64_t n, int64_t k) {
     return size_t(p.chunks) * size_t((n + 15) / 16) * size_t(p.qmax) * 256 * sizeof(float);
 }
 
-// image: the layout's small-M image (kai_launch.h) of the m activation rows.
-template <int TYPE>
+// image: the layout's small-M image (kai_launch.h) of the m activation rows. EXACT: the
+// exact weight products (mmqs_step).
+template <int TYPE, bool EXACT = false>
 void launch_mmqs(const void *weight, int64_t n, int64_t k, int64_t m, const uint8_t *image, const float *inverse,
                  float *partial, size_t partial_bytes, void *dst, bool dst_bf16, int64_t stride_dst,
                  hipStream_t stream) {
@@ -404,7 +407,7 @@ void launch_mmqs(const void *weight, int64_t n, int64_t k, int64_t m, const uint
     const int64_t row_bytes = (k / block_elems(TYPE)) * block_bytes(TYPE);
     if (n * row_bytes >= (int64_t(1) << 32)) throw Error("The small-M GEMM takes matrices below 4 GiB");
     const size_t lds = mmqs_lds_bytes<TYPE>(p);
-    auto kernel = mmqs_kernel<TYPE, MMQS_DEPTH, MMQS_WAVES>;
+    auto kernel = mmqs_kernel<TYPE, MMQS_DEPTH, MMQS_WAVES, EXACT>;
     static DeviceFlags lds_raised;
     raise_dynamic_lds(reinterpret_cast<const void *>(kernel), MMQS_LDS_BUDGET - (TYPE == IQ3_S ? 2048 : 0), lds_raised,
                       "Cannot raise the small-M GEMM's dynamic LDS limit");

@@ -144,6 +144,18 @@ __device__ __forceinline__ BlockCodes quad_codes(const float (&v)[8], int8_t (&q
     return b;
 }
 
+// The quad's share of one Q8_1 block: part 0 writes ds = (hd, hs), each part its 8 codes.
+__device__ __forceinline__ void quad_write(block_q8_1 *out, int part, uint16_t hd, uint16_t hs, const int8_t (&q)[8]) {
+    uint32_t *w = reinterpret_cast<uint32_t *>(out);
+    if (part == 0) w[0] = static_cast<uint32_t>(hd) | (static_cast<uint32_t>(hs) << 16);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        w[1 + 2 * part + i] = static_cast<uint32_t>(static_cast<uint8_t>(q[4 * i])) |
+                              (static_cast<uint32_t>(static_cast<uint8_t>(q[4 * i + 1])) << 8) |
+                              (static_cast<uint32_t>(static_cast<uint8_t>(q[4 * i + 2])) << 16) |
+                              (static_cast<uint32_t>(static_cast<uint8_t>(q[4 * i + 3])) << 24);
+}
+
 // One Q8_1 block from the four lanes of a quad: part 0 writes (d, d * sum), each part
 // its 8 codes. Returns the stored fp16 d.
 __device__ __forceinline__ float quad_store(const float (&v)[8], block_q8_1 *out, int part, int8_t (&q)[8]) {
@@ -151,15 +163,7 @@ __device__ __forceinline__ float quad_store(const float (&v)[8], block_q8_1 *out
     // half(d * sum) rounds the product to fp32 first, then to fp16 (no fused conversion).
     float prod = b.d * static_cast<float>(b.isum);
     __asm__ volatile("" : "+v"(prod));
-    const uint16_t hs = float_to_half_bits(prod);
-    uint32_t *w = reinterpret_cast<uint32_t *>(out);
-    if (part == 0) w[0] = static_cast<uint32_t>(b.hd) | (static_cast<uint32_t>(hs) << 16);
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-        w[1 + 2 * part + i] = static_cast<uint32_t>(static_cast<uint8_t>(q[4 * i])) |
-                              (static_cast<uint32_t>(static_cast<uint8_t>(q[4 * i + 1])) << 8) |
-                              (static_cast<uint32_t>(static_cast<uint8_t>(q[4 * i + 2])) << 16) |
-                              (static_cast<uint32_t>(static_cast<uint8_t>(q[4 * i + 3])) << 24);
+    quad_write(out, part, b.hd, float_to_half_bits(prod), q);
     return half_bits_to_float(b.hd);
 }
 
@@ -184,6 +188,77 @@ __global__ __launch_bounds__(PREP_THREADS) void prepare_q8_1_kernel(
         for (int j = 0; j < 8; ++j) v[j] = fmaf(-d1h, static_cast<float>(q1[j]), v[j]);
         int8_t q2[8];
         quad_store(v, y2 + static_cast<int64_t>(row) * nblocks + ib, part, q2);
+    }
+}
+
+// ---------------------------------------------------------------- legacy activation
+// quantize_q8_1 of the legacy _C_gguf ops (vllm_gguf_plugin/csrc/gguf/gguf_kernel.cu:32-69):
+// no row normalisation; per 32 values d = max|x| / 127 and q = roundf(x / d) as in
+// quad_codes, ds = (half(d), half(sum x)). The reference adds sum x with a 32-lane xor
+// butterfly; lane 0's sum is pass h = 16, 8, 4, 2, 1 adding value i + h to value i (i < h).
+// Lane `part` of a quad holds values 8 part .. 8 part + 7, so passes 16 and 8 pair it with
+// lanes part ^ 2 and part ^ 1 (values i + 16 and i + 8), and passes 4, 2, 1 stay in the
+// lane. Every lane of the quad ends with the same sum (fp32 addition is commutative).
+__device__ __forceinline__ float legacy_block_sum(const float (&v)[8]) {
+    float t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = v[j] + dpp_f32<DPP_QUAD_2301>(v[j]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = t[j] + dpp_f32<DPP_QUAD_1032>(t[j]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t[j] = t[j] + t[j + 4];
+    t[0] = t[0] + t[2];
+    t[1] = t[1] + t[3];
+    return t[0] + t[1];
+}
+
+// Legacy block of the quad: codes, fp16 d and fp16 sum x.
+struct LegacyBlock {
+    int8_t q[8];
+    uint16_t hd, hs;
+};
+__device__ __forceinline__ LegacyBlock legacy_block(const float (&v)[8]) {
+    LegacyBlock b;
+    b.hd = quad_codes(v, b.q).hd;
+    b.hs = float_to_half_bits(legacy_block_sum(v));
+    return b;
+}
+
+// Launch as prepare_q8_1_kernel; inverse[row] = 1 (no normalisation to undo).
+template <int DTYPE>
+__global__ __launch_bounds__(PREP_THREADS) void prepare_legacy_kernel(const typename Src<DTYPE>::T *__restrict__ x,
+                                                                      int64_t stride_x, int k,
+                                                                      block_q8_1 *__restrict__ y,
+                                                                      float *__restrict__ inverse) {
+    const int row = blockIdx.x;
+    const int nblocks = k / QK8_1;
+    const int part = threadIdx.x & 3, ib = blockIdx.y * PREP_BLOCKS + (threadIdx.x >> 2);
+    if (blockIdx.y == 0 && threadIdx.x == 0) inverse[row] = 1.0f;
+    if (ib >= nblocks) return;  // whole quads
+    float v[8];
+    load8<DTYPE>(x + static_cast<int64_t>(row) * stride_x + QK8_1 * ib + 8 * part, v);
+    const LegacyBlock b = legacy_block(v);
+    quad_write(y + static_cast<int64_t>(row) * nblocks + ib, part, b.hd, b.hs, b.q);
+}
+
+template <int DTYPE>
+static void launch_prepare_legacy_dtype(const void *x, int64_t m, int64_t k, int64_t stride_x, const ActLayout &o,
+                                        hipStream_t stream) {
+    const int64_t nblocks = k / QK8_1;
+    const dim3 grid(static_cast<unsigned>(m), static_cast<unsigned>((nblocks + PREP_BLOCKS - 1) / PREP_BLOCKS));
+    prepare_legacy_kernel<DTYPE><<<grid, dim3(PREP_THREADS), 0, stream>>>(
+        static_cast<const typename Src<DTYPE>::T *>(x), stride_x, static_cast<int>(k), o.y1, o.inverse);
+}
+
+void launch_prepare_legacy(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const ActLayout &out,
+                           hipStream_t stream) {
+    if (k <= 0 || k % QK8_1 || k / QK8_1 > int64_t(PREP_BLOCKS) * 65535 || m <= 0 || m > INT_MAX)
+        throw Error("Invalid legacy activation shape");
+    switch (x_dtype) {
+        case 0: launch_prepare_legacy_dtype<0>(x, m, k, stride_x, out, stream); break;
+        case 1: launch_prepare_legacy_dtype<1>(x, m, k, stride_x, out, stream); break;
+        case 2: launch_prepare_legacy_dtype<2>(x, m, k, stride_x, out, stream); break;
+        default: throw Error("Legacy activations must be F32, BF16 or F16");
     }
 }
 
@@ -291,7 +366,55 @@ __device__ __forceinline__ void mmqs_image_lane(const MmqPlanes &p, int ib, int 
     }
 }
 
-template <int DTYPE>
+// The legacy quantisation (legacy_block) into the D4 / DS4 planes or small-M images, for
+// the legacy ops' batched product: D4 holds the stored fp16 d as fp32 (the legacy MMQ reads
+// d8 from the block's half2 ds), DS4 the half2 (d, sum x), and the DS4 image's two min-term
+// factors (Q4_K, Q4_0) are both the stored half(sum x) (vecdotq.cuh:46-66, :353-377).
+__device__ __forceinline__ void legacy_mmq_lane(const MmqPlanes &p, int ib, int row, int m, int part, int k,
+                                                const float (&v)[8]) {
+    if (p.image && ib >= 8 * static_cast<int>(mmqs_steps(k))) return;  // whole quads
+    const LegacyBlock b = legacy_block(v);
+    const uint2 packed = pack_codes(b.q);
+    const float dh = half_bits_to_float(b.hd);
+    if (p.image) {
+        const size_t step = static_cast<size_t>(ib >> 3);
+        const int bb = ib & 7;
+        const int code_at = (bb * 16 + row) * 32 + 8 * (part ^ ((row >> 2) & 3));
+        const int word_at = MMQS_CODE_BYTES + (bb * 16 + row) * 4;
+        if (p.d4) {
+            uint8_t *img = p.d4 + step * mmqs_image_step(MMQ_D4);
+            *reinterpret_cast<uint2 *>(img + code_at) = packed;
+            if (part == 0) *reinterpret_cast<float *>(img + word_at) = dh;
+        }
+        if (p.ds4) {
+            uint8_t *img = p.ds4 + step * mmqs_image_step(MMQ_DS4);
+            *reinterpret_cast<uint2 *>(img + code_at) = packed;
+            if (part == 0) {
+                float *w = reinterpret_cast<float *>(img + word_at);
+                w[0] = dh;
+                w[MMQS_D8_BYTES / 4] = half_bits_to_float(b.hs);
+                w[MMQS_D8_BYTES / 2] = half_bits_to_float(b.hs);
+            }
+        }
+        return;
+    }
+    const int sub = ib & 3;
+    const size_t blk = (static_cast<size_t>(ib >> 2) * static_cast<size_t>(m) + static_cast<size_t>(row)) * MMQ_BLOCK_BYTES;
+    const size_t codes = blk + 16 + 32 * sub + 8 * part;
+    if (p.d4) {
+        *reinterpret_cast<uint2 *>(p.d4 + codes) = packed;
+        if (part == 0) *reinterpret_cast<float *>(p.d4 + blk + 4 * sub) = dh;
+    }
+    if (p.ds4) {
+        *reinterpret_cast<uint2 *>(p.ds4 + codes) = packed;
+        if (part == 0)
+            *reinterpret_cast<uint32_t *>(p.ds4 + blk + 4 * sub) =
+                static_cast<uint32_t>(b.hd) | (static_cast<uint32_t>(b.hs) << 16);
+    }
+}
+
+// LEGACY: the legacy ops' quantisation (no row normalisation, inverse 1, legacy_mmq_lane).
+template <int DTYPE, bool LEGACY>
 __global__ __launch_bounds__(PREP_THREADS) void prepare_mmq_kernel(
     const typename Src<DTYPE>::T *__restrict__ x, int64_t stride_x, int k, int m, int kpad_blocks, MmqPlanes p) {
     __shared__ float wave_max_lds[PREP_THREADS / WAVE];
@@ -301,11 +424,22 @@ __global__ __launch_bounds__(PREP_THREADS) void prepare_mmq_kernel(
     const auto *xr = x + static_cast<int64_t>(row) * stride_x;
     float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
     float scale = 0.0f;
-    if (row < m)  // uniform over the workgroup
+    if constexpr (LEGACY) {
+        if (row < m) {
+            if (blockIdx.y == 0 && threadIdx.x == 0) p.inverse[row] = 1.0f;
+            if (ib < nblocks) load8<DTYPE>(xr + QK8_1 * ib + 8 * part, v);
+            scale = 1.0f;
+        }
+    } else if (row < m) {  // uniform over the workgroup
         scale = row_scale<DTYPE>(xr, k, wave_max_lds, p.inverse + row, blockIdx.y == 0 && threadIdx.x == 0, v);
+    }
     if (ib >= kpad_blocks) return;  // whole groups of 8 lanes (kpad_blocks is a multiple of 16)
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = ib < nblocks ? v[j] * scale : 0.0f;
+    if constexpr (LEGACY) {
+        legacy_mmq_lane(p, ib, row, m, part, k, v);
+        return;
+    }
     if (p.image) {
         if (ib >= 8 * static_cast<int>(mmqs_steps(k))) return;  // whole groups of 8 lanes
         mmqs_image_lane(p, ib, row, part, v);
@@ -376,9 +510,13 @@ static void launch_prepare_mmq_dtype(const void *x, int64_t m, int64_t k, int64_
     const int kpad_blocks = static_cast<int>(mmq_blocks128(k) * 4);
     const int64_t rows = p.image ? MMQS_MAX_ROWS : m;  // images: the zero rows too
     const dim3 grid(static_cast<unsigned>(rows), static_cast<unsigned>((kpad_blocks + PREP_BLOCKS - 1) / PREP_BLOCKS));
-    prepare_mmq_kernel<DTYPE><<<grid, dim3(PREP_THREADS), 0, stream>>>(
-        static_cast<const typename Src<DTYPE>::T *>(x), stride_x, static_cast<int>(k), static_cast<int>(m),
-        kpad_blocks, p);
+    const auto *src = static_cast<const typename Src<DTYPE>::T *>(x);
+    if (p.legacy)
+        prepare_mmq_kernel<DTYPE, true><<<grid, dim3(PREP_THREADS), 0, stream>>>(
+            src, stride_x, static_cast<int>(k), static_cast<int>(m), kpad_blocks, p);
+    else
+        prepare_mmq_kernel<DTYPE, false><<<grid, dim3(PREP_THREADS), 0, stream>>>(
+            src, stride_x, static_cast<int>(k), static_cast<int>(m), kpad_blocks, p);
 }
 
 void launch_prepare_mmq(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const MmqPlanes &planes,
@@ -386,6 +524,7 @@ void launch_prepare_mmq(const void *x, int x_dtype, int64_t m, int64_t k, int64_
     if (k % QK8_1 || k <= 0 || m <= 0 || m > INT_MAX || mmq_blocks128(k) * 4 > INT_MAX)
         throw Error("Invalid batched activation shape");
     if (planes.image && m > MMQS_MAX_ROWS) throw Error("Small-M images hold at most 16 activation rows");
+    if (planes.legacy && planes.d2s6) throw Error("The legacy quantisation has no D2S6 layout");
     switch (x_dtype) {
         case 0: launch_prepare_mmq_dtype<0>(x, m, k, stride_x, planes, stream); break;
         case 1: launch_prepare_mmq_dtype<1>(x, m, k, stride_x, planes, stream); break;

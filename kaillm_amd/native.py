@@ -56,6 +56,14 @@ def _load(path: str):
     lib.kai_upload_rows.restype = c_int
     lib.kai_dequantize.argtypes = [ptr, c_int, i64, i64, ptr, c_int, u64]
     lib.kai_dequantize.restype = c_int
+    lib.kai_ggml_quantize_q8_1.argtypes = [ptr, c_int, i64, i64, i64, ptr, u64]
+    lib.kai_ggml_quantize_q8_1.restype = c_int
+    lib.kai_ggml_a8_workspace.argtypes = [c_int, i64, i64, i64, c_int]
+    lib.kai_ggml_a8_workspace.restype = ctypes.c_size_t
+    for name in ("kai_ggml_mul_mat_vec_a8", "kai_ggml_mul_mat_a8"):
+        getattr(lib, name).argtypes = [ptr, c_int, i64, ptr, c_int, i64, i64, i64, ptr, c_int, ptr, ctypes.c_size_t,
+                                       u64]
+        getattr(lib, name).restype = c_int
     lib.kai_quantize_rows.argtypes = [c_int, ptr, i64, i64, ptr, c_int]
     lib.kai_quantize_rows.restype = c_int
     return lib

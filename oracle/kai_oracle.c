@@ -185,6 +185,49 @@ int oracle_prepare(const void *x, int x_dtype, int64_t m, int64_t k, int64_t str
     return 0;
 }
 
+/* Sum of 32 values as the xor butterfly of gguf_kernel.cu:50-54 leaves it in lane 0:
+ * pass h (16, 8, 4, 2, 1) adds value i + h to value i for i < h. fp32 addition is
+ * commutative, so lane 0's `sum += shfl(sum, h)` is this sum whichever operand is first. */
+static float butterfly_sum32(const float *v) {
+    float t[32];
+    memcpy(t, v, sizeof t);
+    for (int h = 16; h >= 1; h >>= 1)
+        for (int i = 0; i < h; ++i) t[i] = t[i] + t[i + h];
+    return t[0];
+}
+
+/* quantize_q8_1 (gguf_kernel.cu:32-69): per 32 values d = amax / 127,
+ * q = amax == 0 ? 0 : roundf(x / d) (:56-57), ds = (half(d), half(sum x)) (:67-68); no row
+ * normalisation, so inverse = 1. */
+int oracle_prepare_legacy(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x,
+                          void *activation) {
+    if (!x || !activation || m < 1 || k <= 0 || k % QK8_1 || stride_x < k || x_dtype < 0 || x_dtype > 2)
+        return -1;
+    const int64_t nb = k / QK8_1;
+    uint8_t *y = (uint8_t *)activation;
+    float *inverse = (float *)(y + align256((size_t)m * (size_t)nb * Q8_1_BYTES));
+    for (int64_t row = 0; row < m; ++row) {
+        inverse[row] = 1.0f;
+        for (int64_t ib = 0; ib < nb; ++ib) {
+            float v[32];
+            float amax = 0.0f;
+            for (int j = 0; j < 32; ++j) {
+                v[j] = load_x(x, x_dtype, row * stride_x + ib * 32 + j);
+                amax = fmaxf(amax, fabsf(v[j]));
+            }
+            const float d = amax / 127.0f;
+            int8_t q[32];
+            for (int j = 0; j < 32; ++j) q[j] = (int8_t)(amax == 0.0f ? 0.0f : roundf(v[j] / d));
+            uint8_t *blk = y + (row * nb + ib) * Q8_1_BYTES;
+            const uint16_t hd = oracle_float_to_half(d), hs = oracle_float_to_half(butterfly_sum32(v));
+            memcpy(blk, &hd, 2);
+            memcpy(blk + 2, &hs, 2);
+            memcpy(blk + 4, q, 32);
+        }
+    }
+    return 0;
+}
+
 /* ---------------------------------------------------------------- fused producers */
 
 /* Round to nearest even; NaN -> quiet NaN with the sign and top payload bits kept. */
@@ -545,6 +588,45 @@ int oracle_mul_mat(int type, const uint8_t *weight, int64_t n, int64_t k, int64_
         for (int64_t j = 0; j < m; ++j) {
             double acc = row_dot(type, weight + r * row_bytes, k, y1 + j * nb * Q8_1_BYTES);
             if (y2) acc += row_dot(type, weight + r * row_bytes, k, y2 + j * nb * Q8_1_BYTES);
+            out[j * n + r] = (double)inverse[j] * acc;
+        }
+    }
+    return 0;
+}
+
+/* Q4_K superblock against 8 legacy Q8_1 blocks as the legacy MMQ forms it
+ * (vec_dot_q4_K_q8_1_impl_mmq, vecdotq.cuh:353-377):
+ *   d * sum_i d8_i sc_i dot_i - dmin * sum_i s8_i m_i, s8 = the stored half(sum x). */
+static double block_dot_q4k_mmq(const uint8_t *b, const uint8_t *q8) {
+    const double d = rd_half(b), dmin = rd_half(b + 2);
+    uint8_t sc[8], mn[8];
+    q4k_scale_min(b + 4, sc, mn);
+    double sum_d = 0.0, sum_m = 0.0;
+    for (int i = 0; i < 8; ++i) {
+        const uint8_t *blk = q8 + i * Q8_1_BYTES;
+        const int8_t *u = q8_q(blk);
+        int64_t dot = 0;
+        for (int l = 0; l < 32; ++l) dot += (int64_t)q4k_code(b, 32 * i + l) * u[l];
+        sum_d += (double)q8_d(blk) * sc[i] * (double)dot;
+        sum_m += (double)q8_s(blk) * mn[i];
+    }
+    return d * sum_d - dmin * sum_m;
+}
+
+int oracle_mul_mat_legacy(int type, const uint8_t *weight, int64_t n, int64_t k, int64_t m,
+                          const void *activation, int batched, double *out, int threads) {
+    if (!mm_args_ok(type, n, k, m, weight, activation) || !out) return -1;
+    if (!(batched && type == ORACLE_Q4_K)) return oracle_mul_mat(type, weight, n, k, m, activation, 0, out, threads);
+    const int64_t row_bytes = (k / 256) * 144, nb = k / QK8_1;
+    const uint8_t *y = (const uint8_t *)activation;
+    const float *inverse = (const float *)(y + align256((size_t)m * (size_t)nb * Q8_1_BYTES));
+    (void)threads;
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
+    for (int64_t r = 0; r < n; ++r) {
+        for (int64_t j = 0; j < m; ++j) {
+            double acc = 0.0;
+            for (int64_t blk = 0; blk < k / 256; ++blk)
+                acc += block_dot_q4k_mmq(weight + r * row_bytes + blk * 144, y + (j * nb + blk * 8) * Q8_1_BYTES);
             out[j * n + r] = (double)inverse[j] * acc;
         }
     }

@@ -24,7 +24,9 @@
  *     :476-523, :553-573, :1097-1125);
  *   - the fused activation producers kai_dual::prepare_view / prepare_swiglu /
  *     norm_prepare (kai_prepare_ext.cuh:121-251), with their two unspecified steps (exp,
- *     and the order of the norm's sum of squares) fixed as the HIP kernels fix them.
+ *     and the order of the norm's sum of squares) fixed as the HIP kernels fix them;
+ *   - the legacy _C_gguf ops: quantize_q8_1 and the legacy MMVQ / MMQ block forms
+ *     (csrc/gguf/gguf_kernel.cu:32-290, vecdotq.cuh).
  * Each function names the reference lines it follows.
  *
  * Pinning (tests/test_oracle_*.py): fp16/bf16 conversion against numpy; Q8_1
@@ -34,7 +36,9 @@
  * IQ3_S grid against the older vendored table (tests/golden/gen_iq3s_grid.py); the
  * producers against FP64 references (exp within 2 ulp of libm's double exp, RMSNorm
  * within bf16 rounding), the view as a transposed copy prepared by oracle_prepare, and
- * the SwiGLU dtype roundings against numpy's own conversions.
+ * the SwiGLU dtype roundings against numpy's own conversions; the legacy quantiser against
+ * closed forms (ties, signed zero, fp16 overflow / underflow, the butterfly's grouping) and
+ * the legacy products against dense FP64 routes (tests/test_oracle_legacy.py).
  */
 #ifndef KAI_ORACLE_H
 #define KAI_ORACLE_H
@@ -135,6 +139,28 @@ int oracle_prepare_mmq(const void *x, int x_dtype, int64_t m, int64_t k, int64_t
  * MMQ tile loaders form (half(d*sc), half(dmin*m) for Q4_K and Q2_K). */
 int oracle_mul_mat_mmq(int type, const uint8_t *weight, int64_t n, int64_t k, int64_t m,
                        const uint8_t *plane, const float *inverse, double *out, int threads);
+
+/* ---- Legacy _C_gguf ops (csrc/gguf/gguf_kernel.cu:32-290, bound as torch ops
+ * ggml_mul_mat_vec_a8 / ggml_mul_mat_a8 at csrc/torch_bindings.cpp:22-53).
+ *
+ * Activation: quantize_q8_1 (gguf_kernel.cu:32-69), per 32-value block with no row
+ * normalisation: amax = max|x|, d = amax / 127, q = amax == 0 ? 0 : roundf(x / d),
+ * ds = (half(d), half(sum x)), the sum being the kernel's 32-lane xor butterfly (masks 16,
+ * 8, 4, 2, 1; lane 0 ends with ((x0 + x16) + (x8 + x24)) + ... in that grouping). Written
+ * in oracle_prepare's single-pass layout with inverse[row] = 1. The reference spaces its
+ * rows K padded to 512 (:74); the padding blocks are zero and no product reads them, so
+ * the dense layout carries the same products. */
+int oracle_prepare_legacy(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x,
+                          void *activation);
+
+/* Products over a legacy activation, FP64 from exact integer block dots.
+ * batched = 0: ggml_mul_mat_vec_a8's MMVQ block dots (mmvq.cuh:2-39), the same
+ * formulas as oracle_mul_mat. batched = 1: ggml_mul_mat_a8's MMQ block dots (mmq.cuh);
+ * they differ from the MMVQ ones only for Q4_K, whose min term takes the stored
+ * half(sum x) (vecdotq.cuh:353-377: sumf_m += ds8.y * m) where MMVQ takes d8 * sum q
+ * (:328-351). out[j * n + r]. */
+int oracle_mul_mat_legacy(int type, const uint8_t *weight, int64_t n, int64_t k, int64_t m,
+                          const void *activation, int batched, double *out, int threads);
 
 /* Library identity string (build flags), for reports. */
 const char *oracle_build_info(void);

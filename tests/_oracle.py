@@ -60,6 +60,10 @@ def lib():
     o.oracle_prepare_mmq.restype = c_int
     o.oracle_mul_mat_mmq.argtypes = [c_int, ptr, i64, i64, i64, ptr, ptr, ptr, c_int]
     o.oracle_mul_mat_mmq.restype = c_int
+    o.oracle_prepare_legacy.argtypes = [ptr, c_int, i64, i64, i64, ptr]
+    o.oracle_prepare_legacy.restype = c_int
+    o.oracle_mul_mat_legacy.argtypes = [c_int, ptr, i64, i64, i64, ptr, c_int, ptr, c_int]
+    o.oracle_mul_mat_legacy.restype = c_int
     o.oracle_build_info.restype = ctypes.c_char_p
     return o
 
@@ -253,6 +257,31 @@ def mul_mat_mmq(qtype, w, k, plane, inverse, threads=8):
     out = np.empty((m, n), dtype=np.float64)
     assert lib().oracle_mul_mat_mmq(qtype, _p(w), n, k, m, _p(plane), _p(inverse), _p(out), threads) == 0
     return out
+
+
+def prepare_legacy(x, dtype_code=None):
+    """The legacy _C_gguf activation of x [m, k] (float32 / float16 / bf16 bits as uint16)."""
+    x = np.ascontiguousarray(x)
+    if dtype_code is None:
+        dtype_code = _code(x)
+    m, k = x.shape
+    out = np.zeros(activation_bytes(m, k), dtype=np.uint8)
+    assert lib().oracle_prepare_legacy(_p(x), dtype_code, m, k, k, _p(out)) == 0
+    return out
+
+
+def mul_mat_legacy(qtype, w, k, activation, m, batched, threads=8):
+    """ggml_mul_mat_vec_a8 (batched=0) / ggml_mul_mat_a8 (batched=1) in FP64: out [m, n]."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    n = w.shape[0]
+    out = np.empty((m, n), dtype=np.float64)
+    assert lib().oracle_mul_mat_legacy(qtype, _p(w), n, k, m, _p(activation), batched, _p(out), threads) == 0
+    return out
+
+
+def legacy_reference(qtype, w, x, batched, dtype_code=None, threads=8):
+    """The legacy op's result for x [m, k]."""
+    return mul_mat_legacy(qtype, w, x.shape[1], prepare_legacy(x, dtype_code), x.shape[0], batched, threads)
 
 
 def mmq_reference(qtype, w, x, dtype_code=None, threads=8):

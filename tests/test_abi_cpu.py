@@ -194,3 +194,34 @@ def test_quantizer_matches_gguf_closed_forms():
     qs = qs[:, :16] | (qs[:, 16:] << 4)
     want4 = np.concatenate([d4.astype(np.float16).view(np.uint8), qs], axis=1)
     assert np.array_equal(quantize(blocks, O.Q4_0), want4)
+
+
+def test_legacy_op_workspace_and_argument_rules(kai):
+    """kai_ggml_* (gguf_kernel.cu:32-290): the decode route needs the single-pass activation;
+    ggml_mul_mat_a8 on Q4_K / Q8_0 / Q6_K needs the batched path's scratch for one matrix."""
+    for m, k in ((1, 256), (8, 4096), (33, 5120)):
+        for qtype in O.WEIGHT_TYPES:
+            assert kai.kai_ggml_a8_workspace(qtype, 64, k, m, 0) == O.activation_bytes(m, k)
+        for qtype in (O.Q4_0, O.Q2_K):
+            assert kai.kai_ggml_a8_workspace(qtype, 64, k, m, 1) == O.activation_bytes(m, k)
+    for qtype in (O.Q4_K, O.Q8_0, O.Q6_K):
+        for m in (9, 16, 17, 80):
+            arr = lambda t, v: (t * 1)(v)
+            want = kai.kai_fused_mmq_workspace(0, arr(ctypes.c_int, qtype), arr(ctypes.c_int64, 5120), 1, 4096, m, 0)
+            assert kai.kai_ggml_a8_workspace(qtype, 5120, 4096, m, 1) == want > 0
+        assert kai.kai_ggml_a8_workspace(qtype, 5120, 4096, 1, 1) > O.activation_bytes(1, 4096)
+    assert kai.kai_ggml_a8_workspace(O.IQ3_S, 64, 256, 9, 1) == 0
+    assert b"no IQ3_S kernel" in kai.current_direct_error()
+    assert kai.kai_ggml_a8_workspace(O.Q4_K, 66, 256, 9, 1) == 0       # four rows at a time
+    assert kai.kai_ggml_a8_workspace(O.Q4_0, 66, 256, 9, 1) > 0        # decode route: any rows
+    assert kai.kai_ggml_a8_workspace(O.Q8_0, 64, 32800, 1, 0) == 0     # k <= 32768
+    assert kai.kai_ggml_a8_workspace(O.Q8_0, 64, 48, 0, 0) == 0        # no rows
+    dummy = ctypes.c_void_p(16)
+    need = kai.kai_ggml_a8_workspace(O.Q4_K, 64, 256, 3, 0)
+    assert kai.kai_ggml_mul_mat_vec_a8(None, O.Q4_K, 64, dummy, 0, 3, 256, 256, dummy, 0, dummy, need, 0) == -1
+    assert kai.kai_ggml_mul_mat_vec_a8(dummy, O.Q4_K, 64, dummy, 0, 3, 256, 128, dummy, 0, dummy, need, 0) == -1
+    assert kai.kai_ggml_mul_mat_vec_a8(dummy, O.Q4_K, 64, dummy, 0, 3, 256, 256, dummy, 0, dummy, need - 1, 0) == -1
+    assert b"smaller than kai_ggml_a8_workspace" in kai.current_direct_error()
+    assert kai.kai_ggml_mul_mat_a8(dummy, O.IQ3_S, 64, dummy, 0, 3, 256, 256, dummy, 0, dummy, 1 << 20, 0) == -1
+    assert kai.kai_ggml_quantize_q8_1(dummy, 0, 1, 60, 64, dummy, 0) == -1    # k % 32
+    assert kai.kai_ggml_quantize_q8_1(dummy, 0, 1, 64, 32, dummy, 0) == -1    # stride < k

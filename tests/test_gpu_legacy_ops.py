@@ -2,9 +2,13 @@
 
 ggml_dequantize replaces csrc/gguf/gguf_kernel.cu:87-102: bit-exact against the oracle's
 dequantisation (gguf-py's formulas in fp32) rounded to the output type by numpy / torch.
-ggml_mul_mat_vec_a8 / ggml_mul_mat_a8 (gguf_kernel.cu:104-290) and the fused_mul_mat_gguf
-dispatch (quantization/linear.py:40-63) run on the fused kernels: within the path's
-normwise bound of the oracle's FP64 result, plus the output type's rounding.
+The legacy activation (kai_ggml_quantize_q8_1, quantize_q8_1 of gguf_kernel.cu:32-69) is
+bit-exact against oracle_prepare_legacy, special blocks included. ggml_mul_mat_vec_a8 /
+ggml_mul_mat_a8 (gguf_kernel.cu:104-290) are within the path's normwise bound (1e-3, plus
+the output type's rounding) of oracle_mul_mat_legacy's FP64 result; the legacy forms differ
+from the fused path's by 7e-3 (Q4_K on ggml_mul_mat_a8) and 1.6e-2 (Q4_0) on these inputs,
+so the bound tells them apart. The fused_mul_mat_gguf dispatch (quantization/linear.py:40-63)
+is checked against the legacy op it picks.
 """
 import numpy as np
 import pytest
@@ -57,24 +61,112 @@ def test_dequantize_defaults_and_empty(kai):
     assert ggml_dequantize(to_dev(w), O.Q8_0, 0, 64, torch.float32).shape == (0, 64)
 
 
+def _host(x):
+    """Device activation -> (numpy array the oracle reads, dtype code or None)."""
+    xh = x.cpu()
+    if x.dtype == torch.bfloat16:
+        return xh.view(torch.int16).numpy().view(np.uint16), 1
+    return xh.numpy(), None
+
+
+def _special_rows(m, k, dtype, rng):
+    """Random rows with the quantiser's corner cases planted in the first blocks."""
+    x = rng.standard_normal((m, k)).astype(np.float32) * rng.choice([1e-3, 1.0, 30.0], size=(m, 1))
+    if m >= 4 and k >= 64:
+        x[0, :32] = -0.0                                   # sum -0, d 0
+        x[1, :32] = 4000.0                                 # sum overflows fp16 to inf
+        x[2, :32] = 0.0
+        x[2, 0], x[2, 1] = 1e-6, -2e-7                     # d underflows fp16 to 0
+        x[3, :32] = 0.0
+        x[3, 0], x[3, 16], x[3, 1] = 4096.0, -4096.0, 2.0 ** -12   # butterfly grouping: sum 2^-12
+        x[3, 32:64] = 0.0
+        x[3, 32], x[3, 33], x[3, 48] = 4096.0, -4096.0, 2.0 ** -12  # ... and here 0
+    return to_dev(x).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,k", [(1, 32), (5, 96), (33, 5120), (4, 40960)])
+def test_legacy_quantize_bit_exact(kai, dtype, m, k):
+    print(f"legacy quantize {dtype} m={m} k={k}", flush=True)
+    rng = np.random.default_rng(m * 7 + k)
+    wide = _special_rows(m, k + 64, dtype, rng)
+    x = wide[:, :k]                                        # row stride k + 64
+    code = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[dtype]
+    act = torch.empty(kai.kai_fused_activation_bytes(m, k, 0), dtype=torch.uint8, device=DEV)
+    st = kai.kai_ggml_quantize_q8_1(x.data_ptr(), code, m, k, wide.stride(0), act.data_ptr(),
+                                    torch.cuda.current_stream().cuda_stream)
+    assert st == 0, kai.current_direct_error()
+    torch.cuda.synchronize()
+    xh, hcode = _host(x.contiguous())
+    want = O.prepare_legacy(xh, hcode)
+    got = act.cpu().numpy()
+    nb = m * (k // 32) * 36
+    off = (nb + 255) // 256 * 256
+    assert np.array_equal(got[:nb], want[:nb])
+    assert np.array_equal(got[off:off + 4 * m], want[off:off + 4 * m])
+
+
 @pytest.mark.parametrize("qtype", O.WEIGHT_TYPES, ids=lambda t: O.NAMES[t])
-@pytest.mark.parametrize("m", [1, 5, 8, 9, 40])
+@pytest.mark.parametrize("m", [1, 5, 9, 17, 40])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
-def test_mul_mat_a8_against_oracle(kai, qtype, m, dtype):
+@pytest.mark.parametrize("batched", [0, 1], ids=["vec_a8", "a8"])
+def test_legacy_ops_against_oracle(kai, qtype, m, dtype, batched):
     from kaillm_amd.ops import ggml_mul_mat_a8, ggml_mul_mat_vec_a8
 
-    print(f"mul_mat_a8 {O.NAMES[qtype]} m={m} {dtype}", flush=True)
-    rng = np.random.default_rng(qtype * 100 + m)
+    if batched and qtype == O.IQ3_S:
+        pytest.skip("no _C_gguf IQ3_S GEMM: test_legacy_iq3s_gemm_is_the_dequantising_route")
+    print(f"legacy {'ggml_mul_mat_a8' if batched else 'ggml_mul_mat_vec_a8'} {O.NAMES[qtype]} m={m} {dtype}",
+          flush=True)
+    rng = np.random.default_rng(qtype * 100 + m + 7 * batched)
     n, k = 200, 1024
     w = _weights(qtype, n, k, rng, "quantized")
     x = to_dev(rng.standard_normal((m, k)).astype(np.float32)).to(dtype)
-    xh = x.cpu()
-    xb, code = (xh.view(torch.int16).numpy().view(np.uint16), 1) if dtype == torch.bfloat16 else (xh.numpy(), None)
-    ref = O.mul_mat(qtype, w, k, O.prepare(xb, dtype_code=code), m) if m <= 8 else O.mmq_reference(qtype, w, xb, code)
-    op = ggml_mul_mat_vec_a8 if m <= 8 else ggml_mul_mat_a8
+    xh, code = _host(x)
+    ref = O.legacy_reference(qtype, w, xh, batched, code)
+    op = ggml_mul_mat_a8 if batched else ggml_mul_mat_vec_a8
     y = op(to_dev(w), x, qtype, n)
     assert y.dtype == dtype and y.shape == (m, n)
-    assert O.normwise_rel(y.float().cpu().numpy(), ref) <= OUT_TOL[dtype]
+    err = O.normwise_rel(y.float().cpu().numpy(), ref)
+    print(f"  normwise rel err {err:.3e}")
+    assert err <= OUT_TOL[dtype]
+
+
+def test_legacy_gemm_shapes(kai):
+    """Row counts the planes route does not take (Q4_K needs four at a time); the decode
+    route takes any (Q4_0); K above 32768 dequantises."""
+    from kaillm_amd.ops import ggml_mul_mat_a8, ggml_mul_mat_vec_a8
+
+    rng = np.random.default_rng(3)
+    x = to_dev(rng.standard_normal((12, 256)).astype(np.float32))
+    w = _weights(O.Q4_0, 66, 256, rng, "quantized")
+    y = ggml_mul_mat_a8(to_dev(w), x, O.Q4_0, 66)
+    assert O.normwise_rel(y.cpu().numpy(), O.legacy_reference(O.Q4_0, w, x.cpu().numpy(), 1)) <= TOL_F32
+    w = _weights(O.Q4_K, 66, 256, rng, "quantized")
+    with pytest.raises(RuntimeError, match="multiple of four"):
+        ggml_mul_mat_a8(to_dev(w), x, O.Q4_K, 66)
+    assert O.normwise_rel(ggml_mul_mat_vec_a8(to_dev(w), x, O.Q4_K, 66).cpu().numpy(),
+                          O.legacy_reference(O.Q4_K, w, x.cpu().numpy(), 0)) <= TOL_F32
+    kk = 33024
+    w = _weights(O.Q8_0, 16, kk, rng, "quantized")
+    xb = rng.standard_normal((2, kk)).astype(np.float32)
+    y = ggml_mul_mat_vec_a8(to_dev(w), to_dev(xb), O.Q8_0, 16).cpu().numpy()
+    assert O.normwise_rel(y, xb.astype(np.float64) @ O.dequantize(O.Q8_0, w, kk).astype(np.float64).T) <= 1e-5
+
+
+def test_legacy_iq3s_gemm_is_the_dequantising_route(kai):
+    """ops.py:200-208: no _C_gguf IQ3_S GEMM, so the op is x @ dequant(W).T (the reference runs
+    its Triton GEMM of the same product)."""
+    from kaillm_amd.ops import ggml_dequantize, ggml_mul_mat_a8
+
+    rng = np.random.default_rng(9)
+    n, k = 96, 512
+    w = _weights(O.IQ3_S, n, k, rng, "quantized")
+    for dtype, tol in ((torch.float32, 1e-5), (torch.bfloat16, 2.0 ** -7)):
+        x = to_dev(rng.standard_normal((20, k)).astype(np.float32)).to(dtype)
+        y = ggml_mul_mat_a8(to_dev(w), x, O.IQ3_S, n)
+        assert torch.equal(y, x @ ggml_dequantize(to_dev(w), O.IQ3_S, n, k, dtype).T)
+        dense = x.float().cpu().numpy().astype(np.float64) @ O.dequantize(O.IQ3_S, w, k).astype(np.float64).T
+        assert O.normwise_rel(y.float().cpu().numpy(), dense) <= tol
 
 
 def test_fused_mul_mat_gguf_dispatch(kai):
@@ -86,17 +178,22 @@ def test_fused_mul_mat_gguf_dispatch(kai):
     x = torch.randn(3, 96, device=DEV, dtype=torch.float16)
     assert torch.equal(fused_mul_mat_gguf(x, wf, 1), x @ wf.T)
     assert fused_mul_mat_gguf(x[:0], wf, 1).shape == (0, 64)
-    # quantized, small and large batches through the fused kernels
+    # quantized: the legacy ops at the reference's thresholds (160 rows: up to 6 on the GEMV)
     n, k = 160, 2048
     w = _weights(O.Q4_K, n, k, rng, "quantized")
-    for m in (1, 2, 7, 33):
+    for m in (1, 6, 7, 33):
         print(f"fused_mul_mat_gguf Q4_K m={m}", flush=True)
         xm = to_dev(rng.standard_normal((m, k)).astype(np.float16))
-        xn = xm.cpu().numpy()
-        ref = O.mul_mat(O.Q4_K, w, k, O.prepare(xn), m) if m <= 8 else O.mmq_reference(O.Q4_K, w, xn)
+        ref = O.legacy_reference(O.Q4_K, w, xm.cpu().numpy(), int(m > 6))
         y = fused_mul_mat_gguf(xm, to_dev(w), O.Q4_K)
         assert y.dtype == torch.float16
         assert O.normwise_rel(y.float().cpu().numpy(), ref) <= OUT_TOL[torch.float16]
+    # IQ3_S above its threshold (16 rows here) is not an MMQ type: dequantise, then a matmul
+    w = _weights(O.IQ3_S, 64, 512, rng, "quantized")
+    xm = to_dev(rng.standard_normal((17, 512)).astype(np.float32))
+    y = fused_mul_mat_gguf(xm, to_dev(w), O.IQ3_S).cpu().numpy()
+    ref = xm.cpu().numpy().astype(np.float64) @ O.dequantize(O.IQ3_S, w, 512).astype(np.float64).T
+    assert O.normwise_rel(y, ref) <= 1e-5
     # K beyond the fused path's 32768: dequantise, then a matmul (F32 here, so no rounding of x)
     kk = 33024
     w = _weights(O.Q6_K, 24, kk, rng, "quantized")

@@ -1,7 +1,8 @@
 """The apply() surface on the GPU: YAQAMixedLinearMethod building layer.yaqa_parts from a
 GGUF file (yaqa_linear.py:150-405 of the reference), its per-part path, and the
 non-compact GGUFLinearMethod.apply over a merged qweight with shards
-(quantization/linear.py:365-407), each checked against the oracle."""
+(quantization/linear.py:365-407), each checked against the oracle: the fused path's
+arithmetic for the compact parts, the legacy ops' for the non-compact layers."""
 from types import SimpleNamespace
 
 import numpy as np
@@ -24,6 +25,18 @@ def _ref(qtype, w, x_dev):
     if m <= 8:
         return O.mul_mat(qtype, w, k, O.prepare(xs, dtype_code=code), m)
     return O.mmq_reference(qtype, w, xs, code)
+
+
+def _legacy_ref(qtype, w, x_dev, rows):
+    """Oracle result of the non-compact dispatch (quantization/linear.py:40-63) for a matrix of
+    `rows` rows: the legacy ggml_mul_mat_vec_a8 up to mmvq_safe rows, ggml_mul_mat_a8 above."""
+    m = x_dev.shape[0]
+    safe = (8 if rows > 5120 else 16) if qtype == O.IQ3_S else (2 if rows > 5120 else 6)
+    if x_dev.dtype == torch.bfloat16:
+        xs, code = x_dev.view(torch.int16).cpu().numpy().view(np.uint16), 1
+    else:
+        xs, code = x_dev.cpu().numpy(), None
+    return O.legacy_reference(qtype, w, xs, int(m > safe), code)
 
 
 def test_yaqa_mixed_method_from_a_gguf_file(kai, tmp_path):
@@ -132,7 +145,7 @@ def test_gguf_linear_method_non_compact_shards(kai, mixed, m):
     bias = torch.randn(256, device=DEV, dtype=torch.float16)
     y = GGUFLinearMethod().apply(layer, x)
     assert y.shape == (m, 256) and y.dtype == torch.float16
-    ref = np.concatenate([_ref(t, w, x) for _, t, w in shards], axis=1)
+    ref = np.concatenate([_legacy_ref(t, w, x, 256 if not mixed else w.shape[0]) for _, t, w in shards], axis=1)
     assert O.normwise_rel(y.float().cpu().numpy(), ref) <= 2.0 ** -11 + 1e-3   # fp16 output rounding
     assert torch.equal(GGUFLinearMethod().apply(layer, x, bias), y + bias)
 
@@ -147,4 +160,4 @@ def test_gguf_linear_method_unsharded_qweight(kai):
     x = to_dev(rng.standard_normal((4, 768)).astype(np.float32))
     y = GGUFLinearMethod().apply(layer, x)
     assert y.dtype == torch.float32
-    assert O.normwise_rel(y.cpu().numpy(), _ref(O.Q2_K, w, x)) <= 1e-3
+    assert O.normwise_rel(y.cpu().numpy(), _legacy_ref(O.Q2_K, w, x, 96)) <= 1e-3
