@@ -66,6 +66,9 @@ __device__ __forceinline__ void mmqs_step(const lds_u8 *wp, int nvalid, const ui
         W::load(w, wp, oct, nvalid);
         W::fix(w);
     }
+    // ISPLIT: one float scale for the whole step (the superblock's d), applied once at the end
+    // to the step's sum of d8 * (integer block dot); the blocks then need no scale product.
+    v4f_t sacc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int h = 0; h < 8; h += HALF) {
         long aq[HALF], bq[HALF];
@@ -83,6 +86,9 @@ __device__ __forceinline__ void mmqs_step(const lds_u8 *wp, int nvalid, const ui
         for (int u = 0; u < HALF; ++u) {
             if constexpr (MODE == MMQ_BLOCK) {
                 r1[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aq[u], bq[u], zero, 0, 0, 0);
+            } else if constexpr (MODE == MMQ_ISPLIT) {  // first half and whole block
+                r1[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aq[u], first ? bq[u] : 0l, zero, 0, 0, 0);
+                r2[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aq[u], bq[u], zero, 0, 0, 0);
             } else {
                 r1[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aq[u], first ? bq[u] : 0l, zero, 0, 0, 0);
                 r2[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aq[u], first ? 0l : bq[u], zero, 0, 0, 0);
@@ -97,12 +103,12 @@ __device__ __forceinline__ void mmqs_step(const lds_u8 *wp, int nvalid, const ui
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[i] = fmaf(d8[i] * sa, static_cast<float>(r1[u][i]), acc[i]);
             } else if constexpr (MODE == MMQ_ISPLIT) {
-                const float sa = W::template scale<BATCHED>(w, b);
+                // sl * C_lo + sh * C_hi = (sl - sh) * C_lo + sh * C (exact 24-bit integers)
                 const int sl = W::iscale(w, 2 * b), sh = W::iscale(w, 2 * b + 1);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int x = __mul24(sl, r1[u][i]) + __mul24(sh, r2[u][i]);
-                    acc[i] = fmaf(d8[i] * sa, static_cast<float>(x), acc[i]);
+                    const int x = __mul24(sl - sh, r1[u][i]) + __mul24(sh, r2[u][i]);
+                    sacc[i] = fmaf(d8[i], static_cast<float>(x), sacc[i]);
                 }
             } else {
                 const float fl = W::fscale(w, 2 * b), fh = W::fscale(w, 2 * b + 1);
@@ -114,6 +120,11 @@ __device__ __forceinline__ void mmqs_step(const lds_u8 *wp, int nvalid, const ui
             }
         }
         __builtin_amdgcn_sched_barrier(0);  // one phase's results live at a time
+    }
+    if constexpr (MODE == MMQ_ISPLIT) {
+        const float sa = W::template scale<BATCHED>(w, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = fmaf(sa, sacc[i], acc[i]);
     }
     if constexpr (NT > 0) {
         const float *ta = reinterpret_cast<const float *>(base + TA_OFF);
