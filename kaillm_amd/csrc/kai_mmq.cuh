@@ -41,6 +41,8 @@
 // both: D column l%16, rows 4*(l/16) + i.
 #pragma once
 
+#include <type_traits>
+
 #include "kai_mmq_formats.h"
 
 namespace kai {
@@ -96,11 +98,27 @@ constexpr int mmq_buf_bytes() {  // one K step of MT activation rows in LDS
     return 16 * TM * (8 * 32 + 8 * 4 + MmqW<TYPE>::NTERM * 4);
 }
 
+// LDS of a workgroup: the double-buffered activation steps of its k-groups (reused for the
+// K-split sums after the loop), then each wave's weight transpose buffers (TN row tiles of 16
+// rows, MmqsStream).
 template <int TYPE, int TM, int TN, int KS>
-constexpr size_t mmq_lds_bytes() {
+constexpr size_t mmq_act_lds_bytes() {
     const size_t act = size_t(2) * KS * mmq_buf_bytes<TYPE, TM>();
     const size_t red = KS > 1 ? size_t(KS - 1) * (4 / KS) * WAVE * TM * TN * 4 * sizeof(float) : 0;
-    return act > red ? act : red;
+    return ((act > red ? act : red) + 15) / 16 * 16;
+}
+template <int TYPE> constexpr int mmq_tile_tbuf() { return 16 * MmqsStream<TYPE>::SBP + 16; }
+// Formats whose weights go through the coalesced stream: superblocks that are not whole
+// 16-byte units, whose fields are many small pieces (Q6_K 210 bytes, IQ3_S 110). Measured
+// on MI355X against the direct field loads: Q6_K 5120 x 17408 at 8 / 32 / 80 rows -12 / -25
+// / -23 %, 5120 x 6144 at 8 rows -17 %, IQ3_S 5120 x 17408 at 8 rows -42 %; Q4_K
+// 34816 x 5120 +11 % (8 rows) to +22 % (80) and Q2_K +11 % at 512 rows, whose direct loads
+// are whole 16-byte pieces already.
+template <int TYPE> constexpr bool mmq_streamed() { return TYPE == Q6_K || TYPE == IQ3_S; }
+template <int TYPE, int TM, int TN, int KS>
+constexpr size_t mmq_lds_bytes() {
+    return mmq_act_lds_bytes<TYPE, TM, TN, KS>() +
+           (mmq_streamed<TYPE>() ? size_t(MMQ_THREADS / WAVE) * TN * mmq_tile_tbuf<TYPE>() : 0);
 }
 
 // PAIR: up to 8 rows of decode Q8_1 blocks (act: block_q8_1 [m][k/32], k % 256 == 0);
@@ -135,9 +153,6 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
     if constexpr (TYPE == IQ3_S) {
         for (int i = tid; i < 512; i += MMQ_THREADS) grid_lds[i] = mmq_iq3s_grid[i];
     }
-    const uint8_t *wrow[TN];
-#pragma unroll
-    for (int t = 0; t < TN; ++t) wrow[t] = weight + int64_t(min(nrow0 + 16 * t + col, n - 1)) * row_bytes;
 
     // ---- activation staging: global Q8_1 blocks -> registers -> LDS (MFMA layout)
     uint4 aq0[PP], aq1[PP];
@@ -212,14 +227,77 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
         }
     };
 
-    // ---- weights: DEPTH K steps in flight per wave
-    typename W::Raw wr[DEPTH][TN];
-    auto wload = [&](typename W::Raw (&w)[TN], int it) {
-        const int s = it * KS + kg;
-        if (s < steps) {
-            const int nvalid = min(8, nb - 8 * s);  // 32-value blocks of this step inside the row
+    // ---- weights: DEPTH K steps in flight per wave. Direct: each lane loads its fields of
+    // its row (rows past n re-read row n - 1). Streamed (mmq_streamed): the coalesced unit
+    // stream of each row tile (MmqsStream): the lane's units (row u / U, unit u % U) as 32-bit
+    // byte offsets (the launcher checks the matrix is below 4 GiB). Every unit start is clamped
+    // to the matrix's last 16 bytes and its LDS position moved back by as many bytes (0 for a
+    // unit wholly past the end, whose rows are never stored), so no load leaves the matrix:
+    // rows past n, the last unit of a superblock that is not whole units, a short last step.
+    constexpr bool STREAM = mmq_streamed<TYPE>();
+    const uint8_t *wrow[TN];
 #pragma unroll
-            for (int t = 0; t < TN; ++t) W::load(w[t], wrow[t] + int64_t(s) * W::SB, oct, nvalid);
+    for (int t = 0; t < TN; ++t) wrow[t] = weight + int64_t(min(nrow0 + 16 * t + col, n - 1)) * row_bytes;
+    using S = MmqsStream<TYPE>;
+    uint32_t ug[S::UPL];
+    int uoff[S::UPL];
+#pragma unroll
+    for (int i = 0; i < S::UPL; ++i) {
+        const int u = lane + WAVE * i, r = u / S::U, c = u % S::U;
+        const bool real = u < 16 * S::U;
+        ug[i] = real ? static_cast<uint32_t>(r) * static_cast<uint32_t>(row_bytes) + 16 * c : 0u;
+        uoff[i] = real ? r * S::SBP + 16 * c : 16 * S::SBP;  // a spare unit past the 16 rows
+    }
+    const uint32_t tail = static_cast<uint32_t>(int64_t(n) * row_bytes - 16);
+    lds_u8 *tbuf = (lds_u8 *)kai_mmq_lds + mmq_act_lds_bytes<TYPE, TM, TN, KS>() + wave * TN * mmq_tile_tbuf<TYPE>();
+    struct Streamed {
+        uint4 v[TN][S::UPL];
+        uint32_t back[TN];  // 4 bits per unit: the bytes its load start was moved back
+    };
+    struct Direct {
+        typename W::Raw raw[TN];
+    };
+    using Slot = typename std::conditional<STREAM, Streamed, Direct>::type;
+    Slot wr[DEPTH];
+    auto wload = [&](Slot &sl, int it) {
+        if constexpr (STREAM) {
+            const uint32_t step = static_cast<uint32_t>(min(it * KS + kg, steps - 1)) * S::SB;
+#pragma unroll
+            for (int t = 0; t < TN; ++t) {
+                const uint32_t base = static_cast<uint32_t>(nrow0 + 16 * t) * static_cast<uint32_t>(row_bytes) + step;
+                sl.back[t] = 0;
+#pragma unroll
+                for (int i = 0; i < S::UPL; ++i) {
+                    const uint32_t g = base + ug[i], a = min(g, tail), back = g - a;
+                    sl.v[t][i] = load_unaligned<uint4>(weight + a);
+                    sl.back[t] |= (back < 16u ? back : 0u) << (4 * i);
+                }
+            }
+        } else {
+            const int s = it * KS + kg;
+            if (s < steps) {
+                const int nvalid = min(8, nb - 8 * s);  // 32-value blocks of this step inside the row
+#pragma unroll
+                for (int t = 0; t < TN; ++t) W::load(sl.raw[t], wrow[t] + int64_t(s) * W::SB, oct, nvalid);
+            }
+        }
+    };
+    // The step's fields of each row tile: streamed, from the wave's transpose buffer (each wave
+    // writes and reads its own buffer, in order, so no barrier is needed).
+    auto wfields = [&](const Slot &sl, typename W::Raw (&w)[TN], int it) {
+        if constexpr (STREAM) {
+            const int nvalid = min(8, nb - 8 * (it * KS + kg));  // 32-value blocks of the step inside the row
+#pragma unroll
+            for (int t = 0; t < TN; ++t) {
+                lds_u8 *tt = tbuf + t * mmq_tile_tbuf<TYPE>();
+#pragma unroll
+                for (int i = 0; i < S::UPL; ++i)
+                    store_unaligned(tt + uoff[i] - int((sl.back[t] >> (4 * i)) & 15u), sl.v[t][i]);
+                W::load(w[t], tt + col * S::SBP, oct, nvalid);
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < TN; ++t) w[t] = sl.raw[t];
         }
     };
 
@@ -230,8 +308,10 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
         for (int t = 0; t < TN; ++t) acc[a][t] = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     const int aoct = W::act_pos(oct) / 8;  // octet of the activation block this lane multiplies
-    auto compute = [&](typename W::Raw (&w)[TN], int buf, int it) {
+    auto compute = [&](const Slot &sl, int buf, int it) {
         if (it * KS + kg >= steps) return;  // wave-uniform
+        typename W::Raw w[TN];
+        wfields(sl, w, it);
 #pragma unroll
         for (int t = 0; t < TN; ++t) W::fix(w[t]);
         const uint8_t *base = kai_mmq_lds + (buf * KS + kg) * BUF;
@@ -434,6 +514,7 @@ static void launch_mmq_tile(const void *weight, int64_t n, int64_t k, const void
                             const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
     constexpr int MT = PAIR ? 8 : 16 * TM, ROWS = 16 * TN * (4 / KS);
     const int64_t row_bytes = (k / block_elems(TYPE)) * block_bytes(TYPE);
+    if (n * row_bytes >= (int64_t(1) << 32)) throw Error("MMQ takes matrices below 4 GiB");
     const size_t lds = mmq_lds_bytes<TYPE, TM, TN, KS>();
     // weight steps in flight: one. The compiler drains every outstanding load before a
     // step's compute (the loop's branches), so a deeper ring only costs registers and

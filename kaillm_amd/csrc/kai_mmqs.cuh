@@ -135,18 +135,7 @@ __device__ __forceinline__ void mmqs_step(const lds_u8 *wp, int nvalid, const ui
     }
 }
 
-// Coalesced weight stream. One K step of a wave's 16 rows is 16 runs of SB bytes (one per
-// row); each run is read as U 16-byte units (unit c = bytes [16c, 16c + 16) of the run,
-// the last one running into the next run, which is ignored), lane l taking units l, l + 64,
-// ... so that a load instruction reads whole 16-byte pieces of a few contiguous runs. The
-// units go into the wave's LDS transpose buffer (row r at r * SBP) from which each lane reads
-// its MFMA operand fields. (Loading the fields straight from HBM puts 16 rows in every load
-// instruction, and with superblocks of 210 bytes (Q6_K) that halves the achieved bandwidth.)
-template <int TYPE>
-struct MmqsStream {
-    static constexpr int SB = MmqW<TYPE>::SB, U = (SB + 15) / 16, SBP = 16 * U;
-    static constexpr int UPL = (16 * U + WAVE - 1) / WAVE;  // units per lane
-};
+// Weights: the coalesced stream of kai_mmq_formats.h (MmqsStream), 16 rows per wave.
 
 // The work split of a launch (host and device agree on it).
 struct MmqsSplit {
