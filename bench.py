@@ -56,7 +56,8 @@ LEGS = [
     ("C5", "down IQ3_S", IQ3_S, 5120, 17408, (1, 16, 2048)),
 ]
 NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q2_K: "Q2_K", Q4_K: "Q4_K", Q6_K: "Q6_K", IQ3_S: "IQ3_S"}
-GEMV_MAX_ROWS = {Q4_0: 8, Q8_0: 8, Q4_K: 4, Q6_K: 4, IQ3_S: 4, Q2_K: 3}  # kai_launch.h gemv_max_rows
+def gemv_max_rows(qtype, k):  # kai_launch.h gemv_max_rows
+    return {Q4_0: 8, Q8_0: 8, Q4_K: 4, Q6_K: 3 if k >= 12288 else 4, IQ3_S: 4, Q2_K: 3}[qtype]
 
 
 def parse():
@@ -77,10 +78,12 @@ def parse():
     return p.parse_args()
 
 
-def kernel_name(qtype, m):
-    if m > 8:
+def kernel_name(qtype, m, k):
+    if m > 16:
         return "int8 MMQ (kai_fused_mmq_run: GGML MMQ planes + mmq_kernel)"
-    if m <= GEMV_MAX_ROWS[qtype]:
+    if m > 8:
+        return "small-M int8 GEMM (kai_fused_mmq_run: GGML MMQ image + mmqs_kernel + reduction)"
+    if m <= gemv_max_rows(qtype, k):
         return "v_dot4 GEMV (mmvq_kernel)"
     return "paired int8 MMQ tile (mmq_kernel, PAIR)"
 
@@ -239,7 +242,7 @@ def main():
                       "(GEMV up to 4 rows, paired int8 MMQ tile above), activation prepared outside the timing",
             "bytes_per_launch": wb, "avg_launch_us": round(avg_us, 2),
             "by_batch": {str(m): {"us": round(u, 2), "GB/s": round(wb / (u * 1e-6) / 1e9, 1),
-                                  "kernel": kernel_name(qtype, m)} for m, u in kernel_us.items()}}
+                                  "kernel": kernel_name(qtype, m, k)} for m, u in kernel_us.items()}}
     tfile = ROOT / "profiles" / "gemv_q4k_34816x5120_traffic.json"
     if tfile.exists():
         tb = json.loads(tfile.read_text()).get("by_batch", {})
@@ -255,7 +258,7 @@ def main():
         us = r.per_launch_us(key, qtype, n, k, m, args.reps, 2)
         wbytes = weight_bytes(qtype, n, k)
         entry = {"config": cfg, "matrix": f"{mname} {NAMES[qtype]} {n}x{k}", "m": m, "us": round(us, 2),
-                 "kernel": kernel_name(qtype, m), "includes": "activation preparation"}
+                 "kernel": kernel_name(qtype, m, k), "includes": "activation preparation"}
         if m >= 512:
             tops = 2.0 * m * n * k / (us * 1e-6) / 1e12
             entry.update({"TOPS": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4), "bound": "mfma int8"})

@@ -95,13 +95,15 @@ void launch_mmvq(int type, const void *weight, int64_t n, int64_t k, int64_t m, 
                  hipStream_t stream);
 
 // Batched GEMM (int8 MFMA), k % 256 == 0: dst[j*stride_dst + r] as above. kai_fused_mmvq uses
-// it above gemv_max_rows(type) rows; up to there the v_dot4 GEMV is faster (measured on
+// it above gemv_max_rows(type, k) rows; up to there the v_dot4 GEMV is faster (measured on
 // MI355X for every format at 3 to 8 rows on the BASELINE shapes, against the paired 8-row
-// MMQ tile: IQ3_S 5120x17408 at 5-6 rows takes 103-116 us on the GEMV, 65 us on MMQ).
-inline int gemv_max_rows(int type) {
+// MMQ tile: IQ3_S 5120x17408 at 5-6 rows takes 103-116 us on the GEMV, 39 us on MMQ; Q6_K
+// 5120x17408 at 4 rows 46.1 us on the GEMV, 41.3 us on MMQ, but 5120x6144 16.2 against 16.8).
+inline int gemv_max_rows(int type, int64_t k) {
     switch (type) {
         case Q4_0: case Q8_0: return 8;
-        case Q4_K: case Q6_K: case IQ3_S: return 4;
+        case Q6_K: return k >= 12288 ? 3 : 4;
+        case Q4_K: case IQ3_S: return 4;
         default: return 3;
     }
 }
