@@ -168,7 +168,8 @@ template <> struct Unit<Q6_K> {
     struct A { Q32 ua, ub; float d8a, d8b; int sa0, sa1, sb0, sb1; };
     int c, h, p;
     __device__ explicit Unit(int sub) : c(sub), h(sub / 2), p(sub % 2) {}
-    __device__ void load_w(W &w, const uint8_t *blk) const {
+    template <typename P>  // global memory or the GEMV's LDS transpose buffer
+    __device__ void load_w(W &w, P blk) const {
         w.l0 = load_unaligned<uint4>(blk + 32 * c);
         w.l1 = load_unaligned<uint4>(blk + 32 * c + 16);
         w.h0 = load_unaligned<uint4>(blk + 128 + 32 * h);
@@ -286,7 +287,8 @@ template <> struct Unit<IQ3_S> {
     int q;
     const uint32_t *grid;  // LDS
     __device__ Unit(int sub, const uint32_t *lds_grid) : q(sub), grid(lds_grid) {}
-    __device__ void load_w(W &w, const uint8_t *blk) const {
+    template <typename P>  // global memory or the GEMV's LDS transpose buffer
+    __device__ void load_w(W &w, P blk) const {
         w.d = load_unaligned<uint16_t>(blk);
         w.qs = load_unaligned<uint4>(blk + 2 + 16 * q);
         w.qh = load_unaligned<uint16_t>(blk + 66 + 2 * q);
