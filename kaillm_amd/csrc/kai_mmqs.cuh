@@ -326,25 +326,26 @@ __global__ __launch_bounds__(WAVES * WAVE) void mmqs_kernel(
 }
 
 // out[row][c] = inverse[row] * sum over chunks, then pieces (in order), of the partial sums
-// of c's row set. (Combining the pieces in the GEMM itself, by the last wave to finish a row
-// set, needs an agent-scope release and acquire per wave: on MI355X those write back and
-// invalidate the XCD's L2 and made the GEMM six times slower.)
+// of c's row set. One workgroup per row set: thread t adds output (row t / 16, column
+// 16 r + t % 16), so each piece's 16 x 16 sums are one contiguous KiB read by one load and the
+// piece counts are uniform. (Combining the pieces in the GEMM itself, by the last wave to
+// finish a row set, needs an agent-scope release and acquire per wave: on MI355X those write
+// back and invalidate the XCD's L2 and made the GEMM six times slower.)
 static __global__ __launch_bounds__(256) void mmqs_reduce_kernel(const float *__restrict__ partial, MmqsSplit split,
                                                                   int steps, int m, int n,
                                                                   const float *__restrict__ inverse,
                                                                   void *__restrict__ dst, int64_t stride_dst,
                                                                   int dst_bf16) {
-    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= int64_t(m) * n) return;
-    const int row = static_cast<int>(i / n), c = static_cast<int>(i % n), r = c / 16;
+    const int r = blockIdx.x, row = threadIdx.x / 16, c = 16 * r + threadIdx.x % 16;
     const int rowsets = (n + 15) / 16;
     float s = 0.0f;
     for (int ch = 0; ch < split.chunks; ++ch) {
         const int sc = mmqs_chunk_steps(split, steps, ch), sce = mmqs_positions(sc), run = mmqs_run(split, rowsets, sc);
         const int np = (r * sce + sce - 1) / run - (r * sce) / run + 1;
-        const float *p = partial + ((int64_t(ch) * rowsets + r) * split.qmax * 16 + row) * 16 + c % 16;
+        const float *p = partial + (int64_t(ch) * rowsets + r) * split.qmax * 256 + threadIdx.x;
         for (int q = 0; q < np; ++q) s += p[q * 256];
     }
+    if (row >= m || c >= n) return;  // rows past m hold zeros; columns past n are not stored
     const float v = s * inverse[row];
     const int64_t idx = int64_t(row) * stride_dst + c;
     if (dst_bf16) static_cast<uint16_t *>(dst)[idx] = float_to_bf16_bits(v);
@@ -414,8 +415,7 @@ void launch_mmqs(const void *weight, int64_t n, int64_t k, int64_t m, const uint
     kernel<<<dim3(static_cast<unsigned>(p.chunks * p.wgs)), MMQS_WAVES * WAVE, lds, stream>>>(
         static_cast<const uint8_t *>(weight), row_bytes, static_cast<int>(n), static_cast<int>(k), image,
         static_cast<int>(m), inverse, p, partial, dst, stride_dst, dst_bf16 ? 1 : 0);
-    const int64_t total = m * n;
-    mmqs_reduce_kernel<<<static_cast<unsigned>((total + 255) / 256), 256, 0, stream>>>(
+    mmqs_reduce_kernel<<<static_cast<unsigned>((n + 15) / 16), 256, 0, stream>>>(
         partial, p, static_cast<int>(mmqs_steps(k)), static_cast<int>(m), static_cast<int>(n), inverse, dst,
         stride_dst, dst_bf16 ? 1 : 0);
 }
