@@ -531,12 +531,16 @@ static void launch_mmq_tile(const void *weight, int64_t n, int64_t k, const void
                                                dst_bf16 ? 1 : 0);
 }
 
-// Tile choice. Activation tile MT = 16*TM rows: all rows up to 80 (weights streamed
-// once), 64-row tiles beyond (weights re-read per tile, from the last-level cache when
-// the tiles of one weight range run together). Weight rows per workgroup: 16*TN per
-// wave, with KS waves splitting K. The first choice that fills the chip with at least
-// two workgroups per CU wins, trying the full activation tile first; LDS per workgroup
-// stays within 80 KiB so that two fit on a CU.
+// Tile choice. Activation tile MT = 16*TM rows: all rows up to 64 (weights streamed
+// once), 32-row tiles from 65 to 80 rows and 64-row tiles beyond (weights re-read per tile,
+// from the last-level cache when the tiles of one weight range run together). Weight rows
+// per workgroup: 16*TN per wave, with KS waves splitting K. The first choice that fills the
+// chip wins, trying the largest activation tile first: 1.5 workgroups per CU up to 80 rows,
+// 2 beyond; LDS per workgroup stays within 80 KiB so that two fit on a CU. Measured on
+// MI355X against one 80-row tile and 2 workgroups per CU: at 80 rows Q4_K 5120x17408 -17 %,
+// Q6_K -11 %, IQ3_S -26 %, Q2_K 34816x5120 -11 %, Q4_K 34816x5120 -3.5 % (IQ3_S +5 %); at
+// 48 rows Q4_K 5120x17408 -11 %, Q6_K 5120x6144 -7 %; at 24 rows 7168x5120 -9 %; at 64
+// rows 7168x5120 +10 %.
 constexpr bool mmq_allowed(int tm, int ks) { return ks == 1 || (ks == 2 && tm <= 3) || (ks == 4 && tm == 1); }
 
 // PLANES: act is the batched path's plane of the type's layout (kai_fused_mmq_run, any m,
@@ -551,10 +555,10 @@ void launch_mmq_type(const void *weight, int64_t n, int64_t k, int64_t m, const 
     static constexpr int CFG[5][2] = {{2, 1}, {1, 1}, {2, 2}, {1, 2}, {1, 4}};
     // Q4_0 keeps 24 registers of wire bytes per row tile and K step: one tile per wave
     constexpr bool wide = TYPE != Q4_0;
-    const int64_t want = 2 * int64_t(device_cu_count());
+    const int64_t want = PLANES && m <= 80 ? 3 * int64_t(device_cu_count()) / 2 : 2 * int64_t(device_cu_count());
     int tm = 1, tn = 1, ks = 4;
     bool found = false;
-    for (int t = m > 80 ? 4 : static_cast<int>((m + 15) / 16); t >= 1 && !found; --t) {
+    for (int t = m > 80 ? 4 : m > 64 ? 2 : static_cast<int>((m + 15) / 16); t >= 1 && !found; --t) {
         for (const auto &c : CFG) {
             if (!mmq_allowed(t, c[1]) || (c[0] == 2 && !wide)) continue;
             const int64_t rows = 16 * c[0] * (4 / c[1]);
