@@ -60,6 +60,20 @@ def gemv_max_rows(qtype, k):  # kai_launch.h gemv_max_rows
     return {Q4_0: 8, Q8_0: 8, Q4_K: 4, Q6_K: 3 if k >= 12288 else 4, IQ3_S: 4, Q2_K: 3}[qtype]
 
 
+def persistent_decode(n, cus=256):
+    """kai_mmqd.cuh mmqd_suits for the benched shapes (all fit its LDS): whole 16-row sets per
+    workgroup keep the workgroups busy for at least 90 % of the longest one's time."""
+    sets = (n + 15) // 16
+    wgs = min(sets, cus)
+    return sets * 10 >= 9 * wgs * -(-sets // wgs)
+
+
+def gemv_rows(qtype, n, k):  # kai_abi.hip run_decode
+    if persistent_decode(n):  # kai_launch.h gemv_rows_before_persistent
+        return {Q4_0: 6, Q8_0: 6, Q4_K: 3, Q2_K: 2}.get(qtype, gemv_max_rows(qtype, k))
+    return gemv_max_rows(qtype, k)
+
+
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -78,13 +92,15 @@ def parse():
     return p.parse_args()
 
 
-def kernel_name(qtype, m, k):
+def kernel_name(qtype, m, n, k):
     if m > 16:
         return "int8 MMQ (kai_fused_mmq_run: GGML MMQ planes + mmq_kernel)"
     if m > 8:
         return "small-M int8 GEMM (kai_fused_mmq_run: GGML MMQ image + mmqs_kernel + reduction)"
-    if m <= gemv_max_rows(qtype, k):
+    if m <= gemv_rows(qtype, n, k):
         return "v_dot4 GEMV (mmvq_kernel)"
+    if persistent_decode(n):
+        return "persistent paired int8 GEMM (mmqd_kernel)"
     return "paired int8 MMQ tile (mmq_kernel, PAIR)"
 
 
@@ -239,10 +255,10 @@ def main():
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
             "kernel": f"Q4_K gate/up 34816x5120 decode kernel, batch {','.join(map(str, decode))} "
-                      "(GEMV up to 4 rows, paired int8 MMQ tile above), activation prepared outside the timing",
+                      "(GEMV up to 3 rows, persistent paired int8 GEMM above), activation prepared outside the timing",
             "bytes_per_launch": wb, "avg_launch_us": round(avg_us, 2),
             "by_batch": {str(m): {"us": round(u, 2), "GB/s": round(wb / (u * 1e-6) / 1e9, 1),
-                                  "kernel": kernel_name(qtype, m, k)} for m, u in kernel_us.items()}}
+                                  "kernel": kernel_name(qtype, m, n, k)} for m, u in kernel_us.items()}}
     tfile = ROOT / "profiles" / "gemv_q4k_34816x5120_traffic.json"
     if tfile.exists():
         tb = json.loads(tfile.read_text()).get("by_batch", {})
@@ -258,7 +274,7 @@ def main():
         us = r.per_launch_us(key, qtype, n, k, m, args.reps, 2)
         wbytes = weight_bytes(qtype, n, k)
         entry = {"config": cfg, "matrix": f"{mname} {NAMES[qtype]} {n}x{k}", "m": m, "us": round(us, 2),
-                 "kernel": kernel_name(qtype, m, k), "includes": "activation preparation"}
+                 "kernel": kernel_name(qtype, m, n, k), "includes": "activation preparation"}
         if m >= 512:
             tops = 2.0 * m * n * k / (us * 1e-6) / 1e12
             entry.update({"TOPS": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4), "bound": "mfma int8"})

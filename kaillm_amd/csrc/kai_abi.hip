@@ -114,14 +114,20 @@ void run_mmq_group(const void *const *weights, const int *types, const int64_t *
 }
 
 // kai_fused_mmvq's product over a single-pass (or two-pass) activation of m <= 8 rows: the
-// v_dot4 GEMV, or the paired int8 tile above gemv_max_rows(type, k) rows or when the rows do
-// not fit the GEMV's LDS staging.
+// v_dot4 GEMV, or above its rows (or when the rows do not fit its LDS staging) the persistent
+// paired GEMM where it suits the matrix, else the tiled paired kernel (kai_launch.h).
 void run_decode(int type, const void *weight, int64_t n, int64_t k, int64_t m, const kai::ActLayout &l, void *dst,
                 bool dst_bf16, int64_t stride_dst, hipStream_t s) {
-    if (!l.y2 && (m > kai::gemv_max_rows(type, k) || !kai::gemv_one_launch(m, k, 0)) && k % 256 == 0)
-        kai::launch_mmq(type, weight, n, k, m, l.y1, l.inverse, dst, dst_bf16, stride_dst, s);
-    else
-        kai::launch_mmvq(type, weight, n, k, m, l.y1, l.y2, l.inverse, dst, dst_bf16, stride_dst, s);
+    if (!l.y2 && k % 256 == 0) {
+        const bool persistent = kai::mmq_decode_persistent(type, n, k);
+        const int gemv_rows = persistent ? kai::gemv_rows_before_persistent(type, k) : kai::gemv_max_rows(type, k);
+        if (m > gemv_rows || !kai::gemv_one_launch(m, k, 0)) {
+            if (persistent) kai::launch_mmq_decode(type, weight, n, k, m, l.y1, l.inverse, dst, dst_bf16, stride_dst, s);
+            else kai::launch_mmq(type, weight, n, k, m, l.y1, l.inverse, dst, dst_bf16, stride_dst, s);
+            return;
+        }
+    }
+    kai::launch_mmvq(type, weight, n, k, m, l.y1, l.y2, l.inverse, dst, dst_bf16, stride_dst, s);
 }
 
 // The legacy ops (csrc/gguf/gguf_kernel.cu:104-290). ggml_mul_mat_a8 on Q4_K, Q8_0 and Q6_K

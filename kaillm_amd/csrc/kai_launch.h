@@ -94,11 +94,19 @@ void launch_mmvq(int type, const void *weight, int64_t n, int64_t k, int64_t m, 
                  const block_q8_1 *y2, const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst,
                  hipStream_t stream);
 
-// Batched GEMM (int8 MFMA), k % 256 == 0: dst[j*stride_dst + r] as above. kai_fused_mmvq uses
-// it above gemv_max_rows(type, k) rows; up to there the v_dot4 GEMV is faster (measured on
-// MI355X for every format at 3 to 8 rows on the BASELINE shapes, against the paired 8-row
-// MMQ tile: IQ3_S 5120x17408 at 5-6 rows takes 103-116 us on the GEMV, 39 us on MMQ; Q6_K
-// 5120x17408 at 4 rows 46.1 us on the GEMV, 41.3 us on MMQ, but 5120x6144 16.2 against 16.8).
+// Products of more decode rows than the GEMV takes (k % 256 == 0), on int8 MFMA with the
+// paired tile's arithmetic (two 32-value blocks per MFMA): the persistent paired GEMM
+// (kai_mmqd.cuh: the activation staged once per workgroup, no scratch) where
+// mmq_decode_persistent(type, n, k), the tiled paired kernel (launch_mmq) elsewhere.
+// kai_fused_mmvq keeps the v_dot4 GEMV up to gemv_max_rows(type, k) rows before the tiled
+// kernel and up to gemv_rows_before_persistent(type, k) before the persistent one. Measured on
+// MI355X for every format at 1 to 8 rows on the BASELINE shapes: against the tiled kernel,
+// IQ3_S 5120x17408 at 5-6 rows takes 103-116 us on the GEMV, 39 us tiled; Q6_K 5120x17408 at 4
+// rows 40.8 / 37.4, but 5120x6144 16.1 / 16.4; Q4_K 7168x5120 at 4 rows 11.2 / 12.1. Against the
+// persistent kernel (34816x5120): Q4_K at 3 / 4 rows 28.4 / 31.8 us on the GEMV, 28.5 / 28.6
+// persistent; Q2_K at 2 / 3 rows 27.5 / 33.7, 28.2 / 28.3; IQ3_S at 4 / 5 rows 39.6 / 57.6,
+// 43.4 / 42.8; Q4_0 16384x2048 at 6 / 8 rows 12.2 / 17.3, 14.7 / 15.0, 2048x8192 14.3 / 27.9,
+// 15.3 / 15.7.
 inline int gemv_max_rows(int type, int64_t k) {
     switch (type) {
         case Q4_0: case Q8_0: return 8;
@@ -107,13 +115,25 @@ inline int gemv_max_rows(int type, int64_t k) {
         default: return 3;
     }
 }
+inline int gemv_rows_before_persistent(int type, int64_t k) {
+    switch (type) {
+        case Q4_0: case Q8_0: return 6;
+        case Q4_K: return 3;
+        case Q2_K: return 2;
+        default: return gemv_max_rows(type, k);
+    }
+}
 // Whether m activation rows fit the GEMV's LDS staging in one launch (more rows are split
 // into launches that each stream the weights again).
 inline bool gemv_one_launch(int64_t m, int64_t k, int two_pass) {
     return m * (two_pass ? 2 : 1) * (k / QK8_1) * 40 <= 160 * 1024 - 4096;
 }
+// dst[j*stride_dst + r] = inverse[j] * sum_b dot(W[r, b], y[j, b]) for j < m <= 8, k % 256 == 0.
 void launch_mmq(int type, const void *weight, int64_t n, int64_t k, int64_t m, const block_q8_1 *y,
                 const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream);
+bool mmq_decode_persistent(int type, int64_t n, int64_t k);
+void launch_mmq_decode(int type, const void *weight, int64_t n, int64_t k, int64_t m, const block_q8_1 *y,
+                       const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream);
 // A batched product over the batched path's activation of the type's layout (any k that
 // is a whole number of the type's blocks): up to MMQS_MAX_ROWS rows on the small-M GEMM
 // (kai_mmqs.cuh) reading the layout's small-M image, which may need

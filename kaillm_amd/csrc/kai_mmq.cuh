@@ -121,6 +121,95 @@ constexpr size_t mmq_lds_bytes() {
            (mmq_streamed<TYPE>() ? size_t(MMQ_THREADS / WAVE) * TN * mmq_tile_tbuf<TYPE>() : 0);
 }
 
+// Row r, block b (0..7) of one staged K step of MT activation rows: the codes at
+// (b*MT + r)*32 with the four 8-byte octets placed at position oct ^ ((r >> 2) & 3), so that
+// the A-operand reads of a wave (16 rows x 4 octets) hit distinct banks; d8 at [b][r]; the
+// min-term factors at [term][r] (one per block, or two for per-16 terms).
+template <int TYPE, int MT>
+__device__ __forceinline__ void stage_block(uint8_t *base, int r, int b, uint4 q0, uint4 q1, float d8,
+                                            const float (&t)[2]) {
+    constexpr int NT = MmqW<TYPE>::NTERM, D8_OFF = MT * 8 * 32, TA_OFF = D8_OFF + MT * 8 * 4;
+    const int sw = (r >> 2) & 3;
+    uint4 *q = reinterpret_cast<uint4 *>(base + (b * MT + r) * 32);
+    const uint4 h0 = sw & 1 ? make_uint4(q0.z, q0.w, q0.x, q0.y) : q0;
+    const uint4 h1 = sw & 1 ? make_uint4(q1.z, q1.w, q1.x, q1.y) : q1;
+    q[sw >> 1] = h0;
+    q[(sw >> 1) ^ 1] = h1;
+    reinterpret_cast<float *>(base + D8_OFF)[b * MT + r] = d8;
+    if constexpr (NT > 0) {
+        float *ta = reinterpret_cast<float *>(base + TA_OFF);
+        if constexpr (NT == 8) {
+            ta[b * MT + r] = t[0];
+        } else {
+            ta[(2 * b) * MT + r] = t[0];
+            ta[(2 * b + 1) * MT + r] = t[1];
+        }
+    }
+}
+
+// One K step of the paired tile (up to 8 activation rows; decode arithmetic) for TN tiles of
+// 16 weight rows: w holds each tile's fields of the step (after fix), base the step's
+// activation in LDS in the paired layout (MT = 8: codes [block][row][32] with the octet
+// swizzle, d8 [block][row], min-term factors [term][row]).
+// PHASED: each pair of blocks in its own scheduling section, so that one pair's operands and
+// MFMA results are live at a time (without it the persistent kernel's Q6_K loop spills).
+template <int TYPE, int TN, bool PHASED = false>
+__device__ __forceinline__ void paired_step(const typename MmqLoad<TYPE>::Raw (&w)[TN], const uint8_t *base,
+                                            v4f_t (&acc)[TN], int col, int oct, int aoct, const uint32_t *grid) {
+    using W = MmqLoad<TYPE>;
+    constexpr int MODE = W::template mode<false>();
+    constexpr int MT = 8, NT = W::NTERM, D8_OFF = MT * 8 * 32, TA_OFF = D8_OFF + MT * 8 * 4;
+    const float *d8s = reinterpret_cast<const float *>(base + D8_OFF);
+    const v4i_t zero = {0, 0, 0, 0};
+    // lane's A row: activation row col % 8 of block 2c + col / 8; its D rows
+    // 4*oct .. +4: activation rows 4*(oct % 2) .. +4 of block 2c + oct / 2
+    const int mr = col & 7, hi = col >> 3, ob = oct >> 1;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint64_t aq =
+            *reinterpret_cast<const uint64_t *>(base + ((2 * c + hi) * MT + mr) * 32 + 8 * (aoct ^ ((mr >> 2) & 3)));
+        const int a0 = static_cast<int>(aq), a1 = static_cast<int>(aq >> 32);
+        const v4i_t av = hi ? v4i_t{0, 0, a0, a1} : v4i_t{a0, a1, 0, 0};
+        const float4 dv = *reinterpret_cast<const float4 *>(d8s + (2 * c + ob) * MT + 4 * (oct & 1));
+        const float d8[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+        for (int t = 0; t < TN; ++t) {
+            const uint64_t c0 = W::template codes<false>(w[t], 2 * c, oct, grid),
+                           c1 = W::template codes<false>(w[t], 2 * c + 1, oct, grid);
+            const v4i_t bv = {static_cast<int>(c0), static_cast<int>(c0 >> 32), static_cast<int>(c1),
+                              static_cast<int>(c1 >> 32)};
+            const float sa = ob ? W::template scale<false>(w[t], 2 * c + 1) : W::template scale<false>(w[t], 2 * c);
+            if constexpr (MODE == MMQ_ISPLIT) {
+                const bool first = W::first_half(oct);
+                const v4i_t r1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, first ? bv : zero, zero, 0, 0, 0);
+                const v4i_t r2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, first ? zero : bv, zero, 0, 0, 0);
+                const int sl = ob ? W::iscale(w[t], 4 * c + 2) : W::iscale(w[t], 4 * c);
+                const int sh = ob ? W::iscale(w[t], 4 * c + 3) : W::iscale(w[t], 4 * c + 1);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int x = __mul24(sl, r1[i]) + __mul24(sh, r2[i]);
+                    acc[t][i] = fmaf(d8[i] * sa, static_cast<float>(x), acc[t][i]);
+                }
+            } else {
+                const v4i_t r = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, zero, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(d8[i] * sa, static_cast<float>(r[i]), acc[t][i]);
+            }
+        }
+        if constexpr (PHASED) __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (NT > 0) {  // the terms go to D rows 0-7 (activation rows 0-7), A rows 8-15 zero
+        const float *ta = reinterpret_cast<const float *>(base + TA_OFF);
+#pragma unroll
+        for (int j = 0; j < NT / 4; ++j) {
+            const float at = col < 8 ? ta[(4 * j + oct) * MT + col] : 0.0f;
+#pragma unroll
+            for (int t = 0; t < TN; ++t)
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(at, W::template term<false>(w[t], j, oct), acc[t], 0, 0, 0);
+        }
+    }
+}
+
 // PAIR: up to 8 rows of decode Q8_1 blocks (act: block_q8_1 [m][k/32], k % 256 == 0);
 // otherwise the batched path's plane of the type's layout (act: uint8 plane), any k that is
 // a whole number of blocks (a short last step reads zero activations).
@@ -190,22 +279,13 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
             }
         }
     };
-    // Codes of row r, block b: 32 bytes at (b*MT + r)*32 with the four 8-byte octets
-    // placed at position oct ^ ((r >> 2) & 3), so that the A-operand reads of a wave
-    // (16 rows x 4 octets) hit distinct banks.
+    // the staged step in the MFMA layout (stage_block)
     auto astore = [&](int buf) {
 #pragma unroll
         for (int p = 0; p < PP; ++p) {
             const int idx = tid + p * MMQ_THREADS;
             if (idx < PAIRS) {
                 const int r = idx % MT, b = (idx / MT) % 8, g = idx / (MT * 8);
-                const int sw = (r >> 2) & 3;
-                uint8_t *base = kai_mmq_lds + (buf * KS + g) * BUF;
-                uint4 *q = reinterpret_cast<uint4 *>(base + (b * MT + r) * 32);
-                const uint4 h0 = sw & 1 ? make_uint4(aq0[p].z, aq0[p].w, aq0[p].x, aq0[p].y) : aq0[p];
-                const uint4 h1 = sw & 1 ? make_uint4(aq1[p].z, aq1[p].w, aq1[p].x, aq1[p].y) : aq1[p];
-                q[sw >> 1] = h0;
-                q[(sw >> 1) ^ 1] = h1;
                 float d8, t[2];
                 if constexpr (PAIR) {
                     d8 = half_bits_to_float(ads[p] & 0xffffu);
@@ -213,16 +293,7 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
                 } else {
                     d8 = plane_terms<TYPE>(aq0[p], aq1[p], ads[p], ads2[p], b, t);
                 }
-                reinterpret_cast<float *>(base + D8_OFF)[b * MT + r] = d8;
-                if constexpr (NT > 0) {
-                    float *ta = reinterpret_cast<float *>(base + TA_OFF);
-                    if constexpr (NT == 8) {
-                        ta[b * MT + r] = t[0];
-                    } else {
-                        ta[(2 * b) * MT + r] = t[0];
-                        ta[(2 * b + 1) * MT + r] = t[1];
-                    }
-                }
+                stage_block<TYPE, MT>(kai_mmq_lds + (buf * KS + g) * BUF, r, b, aq0[p], aq1[p], d8, t);
             }
         }
     };
@@ -318,45 +389,11 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
         const float *d8s = reinterpret_cast<const float *>(base + D8_OFF);
         const v4i_t zero = {0, 0, 0, 0};
         if constexpr (PAIR) {
-            // lane's A row: activation row col % 8 of block 2c + col / 8; its D rows
-            // 4*oct .. +4: activation rows 4*(oct % 2) .. +4 of block 2c + oct / 2
-            const int mr = col & 7, hi = col >> 3, ob = oct >> 1;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const uint64_t aq =
-                    *reinterpret_cast<const uint64_t *>(base + ((2 * c + hi) * MT + mr) * 32 + 8 * (aoct ^ ((mr >> 2) & 3)));
-                const int a0 = static_cast<int>(aq), a1 = static_cast<int>(aq >> 32);
-                const v4i_t av = hi ? v4i_t{0, 0, a0, a1} : v4i_t{a0, a1, 0, 0};
-                const float4 dv = *reinterpret_cast<const float4 *>(d8s + (2 * c + ob) * MT + 4 * (oct & 1));
-                const float d8[4] = {dv.x, dv.y, dv.z, dv.w};
-#pragma unroll
-                for (int t = 0; t < TN; ++t) {
-                    const uint64_t c0 = W::template codes<false>(w[t], 2 * c, oct, grid_lds),
-                                   c1 = W::template codes<false>(w[t], 2 * c + 1, oct, grid_lds);
-                    const v4i_t bv = {static_cast<int>(c0), static_cast<int>(c0 >> 32), static_cast<int>(c1),
-                                      static_cast<int>(c1 >> 32)};
-                    const float sa = ob ? W::template scale<false>(w[t], 2 * c + 1) : W::template scale<false>(w[t], 2 * c);
-                    if constexpr (MODE == MMQ_ISPLIT) {
-                        const bool first = W::first_half(oct);
-                        const v4i_t r1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, first ? bv : zero, zero, 0, 0, 0);
-                        const v4i_t r2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, first ? zero : bv, zero, 0, 0, 0);
-                        const int sl = ob ? W::iscale(w[t], 4 * c + 2) : W::iscale(w[t], 4 * c);
-                        const int sh = ob ? W::iscale(w[t], 4 * c + 3) : W::iscale(w[t], 4 * c + 1);
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const int x = __mul24(sl, r1[i]) + __mul24(sh, r2[i]);
-                            acc[0][t][i] = fmaf(d8[i] * sa, static_cast<float>(x), acc[0][t][i]);
-                        }
-                    } else {
-                        const v4i_t r = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, zero, 0, 0, 0);
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) acc[0][t][i] = fmaf(d8[i] * sa, static_cast<float>(r[i]), acc[0][t][i]);
-                    }
-                }
-            }
+            paired_step<TYPE, TN>(w, base, acc[0], col, oct, aoct, grid_lds);
+            return;
         }
 #pragma unroll
-        for (int b = 0; b < (PAIR ? 0 : 8); ++b) {
+        for (int b = 0; b < 8; ++b) {
             uint64_t bq[TN], bq2[TN];
             float sa[TN], fl[TN], fh[TN];
             int sl[TN], sh[TN];
@@ -419,9 +456,7 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
                 for (int t = 0; t < TN; ++t) bt[t] = W::template term<BATCHED>(w[t], j, oct);
 #pragma unroll
                 for (int a = 0; a < TM; ++a) {
-                    // paired: the terms go to D rows 0-7 (activation rows 0-7), A rows 8-15 zero
-                    const float at = PAIR ? (col < 8 ? ta[(4 * j + oct) * MT + col] : 0.0f)
-                                          : ta[(4 * j + oct) * MT + 16 * a + col];
+                    const float at = ta[(4 * j + oct) * MT + 16 * a + col];
 #pragma unroll
                     for (int t = 0; t < TN; ++t) acc[a][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(at, bt[t], acc[a][t], 0, 0, 0);
                 }

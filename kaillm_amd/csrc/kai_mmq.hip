@@ -1,5 +1,5 @@
 // MMQ dispatch by weight type (instantiations live in kai_mmq_<type>.hip).
-#include "kai_mmqs.cuh"
+#include "kai_mmqd.cuh"
 
 namespace kai {
 
@@ -10,7 +10,9 @@ namespace kai {
     extern template void launch_mmq_type<T, true>(const void *, int64_t, int64_t, int64_t, const void *, \
                                                   const float *, void *, bool, int64_t, hipStream_t); \
     extern template void launch_mmqs<T>(const void *, int64_t, int64_t, int64_t, const uint8_t *, const float *, \
-                                        float *, size_t, void *, bool, int64_t, hipStream_t);
+                                        float *, size_t, void *, bool, int64_t, hipStream_t); \
+    extern template void launch_mmqd<T>(const void *, int64_t, int64_t, int64_t, const block_q8_1 *, const float *, \
+                                        void *, bool, int64_t, hipStream_t);
 KAI_EXTERN(Q8_0) KAI_EXTERN(Q4_0) KAI_EXTERN(Q4_K) KAI_EXTERN(Q6_K) KAI_EXTERN(Q2_K) KAI_EXTERN(IQ3_S)
 #undef KAI_EXTERN
 extern template void launch_mmq_type<Q4_K, true, true>(const void *, int64_t, int64_t, int64_t, const void *,
@@ -33,6 +35,25 @@ static void dispatch(int type, const void *weight, int64_t n, int64_t k, int64_t
 void launch_mmq(int type, const void *weight, int64_t n, int64_t k, int64_t m, const block_q8_1 *y,
                 const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
     dispatch<false>(type, weight, n, k, m, y, inverse, dst, dst_bf16, stride_dst, stream);
+}
+
+bool mmq_decode_persistent(int type, int64_t n, int64_t k) {
+    switch (type) {
+#define KAI_T(T) case T: return mmqd_suits<T>(n, k, device_cu_count());
+        KAI_T(Q8_0) KAI_T(Q4_0) KAI_T(Q4_K) KAI_T(Q6_K) KAI_T(Q2_K) KAI_T(IQ3_S)
+#undef KAI_T
+        default: return false;
+    }
+}
+
+void launch_mmq_decode(int type, const void *weight, int64_t n, int64_t k, int64_t m, const block_q8_1 *y,
+                       const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
+    switch (type) {
+#define KAI_T(T) case T: launch_mmqd<T>(weight, n, k, m, y, inverse, dst, dst_bf16, stride_dst, stream); break;
+        KAI_T(Q8_0) KAI_T(Q4_0) KAI_T(Q4_K) KAI_T(Q6_K) KAI_T(Q2_K) KAI_T(IQ3_S)
+#undef KAI_T
+        default: throw Error("Unsupported fused MMQ weight type");
+    }
 }
 
 void launch_mmq_planes(int type, const void *weight, int64_t n, int64_t k, int64_t m, const uint8_t *plane,

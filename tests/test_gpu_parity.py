@@ -348,9 +348,9 @@ PAIRED = [(O.Q4_K, 5, 768, 200), (O.Q6_K, 8, 1280, 136), (O.Q2_K, 6, 768, 200), 
 @pytest.mark.parametrize("qtype,m,k,n", PAIRED, ids=lambda v: str(v))
 @pytest.mark.parametrize("bf16", [False, True])
 def test_mmq_paired_tile(kai, qtype, m, k, n, bf16):
-    """Up to 8 rows on the int8-MFMA GEMM (two 32-value blocks per MFMA), reached through
-    kai_fused_mmvq above the GEMV's row limit or, for the 8-row GEMV formats, above its
-    LDS staging (long K): partial weight tiles, K split over waves, strided bf16 output."""
+    """Up to 8 rows on int8 MFMA (two 32-value blocks per MFMA), reached through
+    kai_fused_mmvq above the GEMV's row limit: on these few row sets the persistent paired
+    GEMM (one workgroup per set; long K in chunks), ragged row sets, strided bf16 output."""
     print(f"mmq paired {O.NAMES[qtype]} m={m} k={k} n={n} bf16={bf16}", flush=True)
     rng = np.random.default_rng(qtype * 100 + m)
     w = O.random_blocks(qtype, n, k, rng)
@@ -362,6 +362,48 @@ def test_mmq_paired_tile(kai, qtype, m, k, n, bf16):
     assert O.normwise_rel(got[:, :n], ref) <= (TOL_BF16 if bf16 else TOL_F32)
     if bf16:
         assert np.isnan(got[:, n:]).all()
+
+
+# Above the GEMV's rows kai_fused_mmvq runs the persistent paired GEMM where whole 16-row sets
+# per workgroup keep the workgroups busy (kai_mmqd.cuh mmqd_suits: under 256 row sets, or
+# at least 90 % busy), the tiled paired kernel elsewhere (kai_abi.hip run_decode).
+# 1000 row sets on 256 CUs: workgroups of 3 and of 4 sets; k = 61 K steps, staged in two
+# chunks of 31 (rounded up to 32 by a zero step) and 30; 15995 rows: the last set ragged.
+PERSISTENT = [(O.Q4_K, 7), (O.Q6_K, 5), (O.Q2_K, 8), (O.IQ3_S, 6), (O.Q8_0, 8), (O.Q4_0, 7)]
+
+
+@pytest.mark.parametrize("qtype,m", PERSISTENT, ids=lambda v: str(v))
+def test_persistent_decode_chunks_and_ragged_sets(kai, qtype, m):
+    n, k = 15995, 61 * 256
+    print(f"persistent decode {O.NAMES[qtype]} m={m} n={n} k={k}", flush=True)
+    rng = np.random.default_rng(qtype * 10 + m)
+    w = O.random_blocks(qtype, n, k, rng)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    act = gpu_prepare(kai, to_dev(x))
+    w_dev = to_dev(w)
+    out = gpu_mmvq(kai, qtype, w_dev, n, k, act, m)
+    again = gpu_mmvq(kai, qtype, w_dev, n, k, act, m)
+    assert torch.equal(out, again), "the slot sums are added in a fixed order"
+    ref = O.mul_mat(qtype, w, k, O.prepare(x), m, threads=16)
+    assert O.normwise_rel(out.cpu().numpy(), ref) <= TOL_F32
+
+
+# C3 shapes whose row sets do not balance over the CUs (448 and 320 sets) stay on the tiled
+# paired kernel: qkv at 8 rows, o_proj at 5, down at 4 (K split over the waves).
+TILED = [(O.Q4_K, 8, 7168, 5120), (O.Q6_K, 5, 5120, 6144), (O.Q6_K, 4, 5120, 17408)]
+
+
+@pytest.mark.parametrize("qtype,m,n,k", TILED, ids=lambda v: str(v))
+def test_tiled_paired_decode_full_shapes(kai, qtype, m, n, k):
+    print(f"tiled paired {O.NAMES[qtype]} m={m} n={n} k={k}", flush=True)
+    rng = np.random.default_rng(n + k + m)
+    w = O.random_blocks(qtype, n, k, rng)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    act = gpu_prepare(kai, to_dev(x))
+    out = gpu_mmvq(kai, qtype, to_dev(w), n, k, act, m, bf16=True, stride=n + 8).float().cpu().numpy()
+    ref = O.mul_mat(qtype, w, k, O.prepare(x), m, threads=16)
+    assert O.normwise_rel(out[:, :n], ref) <= TOL_BF16
+    assert np.isnan(out[:, n:]).all()
 
 
 @pytest.mark.parametrize("qtype", [O.Q4_K, O.Q6_K, O.IQ3_S])
