@@ -12,13 +12,17 @@ namespace kai {
     extern template void launch_mmqs<T>(const void *, int64_t, int64_t, int64_t, const uint8_t *, const float *, \
                                         float *, size_t, void *, bool, int64_t, hipStream_t); \
     extern template void launch_mmqd<T>(const void *, int64_t, int64_t, int64_t, const block_q8_1 *, const float *, \
-                                        void *, bool, int64_t, hipStream_t);
+                                        void *, bool, int64_t, hipStream_t); \
+    extern template void launch_mmqd_image<T>(const void *, int64_t, int64_t, int64_t, const uint8_t *, const float *, \
+                                              void *, bool, int64_t, hipStream_t);
 KAI_EXTERN(Q8_0) KAI_EXTERN(Q4_0) KAI_EXTERN(Q4_K) KAI_EXTERN(Q6_K) KAI_EXTERN(Q2_K) KAI_EXTERN(IQ3_S)
 #undef KAI_EXTERN
 extern template void launch_mmq_type<Q4_K, true, true>(const void *, int64_t, int64_t, int64_t, const void *,
                                                        const float *, void *, bool, int64_t, hipStream_t);
 extern template void launch_mmqs<Q4_K, true>(const void *, int64_t, int64_t, int64_t, const uint8_t *, const float *,
                                              float *, size_t, void *, bool, int64_t, hipStream_t);
+extern template void launch_mmqd_image<Q4_K, true>(const void *, int64_t, int64_t, int64_t, const uint8_t *,
+                                                   const float *, void *, bool, int64_t, hipStream_t);
 
 template <bool PLANES>
 static void dispatch(int type, const void *weight, int64_t n, int64_t k, int64_t m, const void *act,
@@ -39,7 +43,7 @@ void launch_mmq(int type, const void *weight, int64_t n, int64_t k, int64_t m, c
 
 bool mmq_decode_persistent(int type, int64_t n, int64_t k) {
     switch (type) {
-#define KAI_T(T) case T: return mmqd_suits<T>(n, k, device_cu_count());
+#define KAI_T(T) case T: return mmqd_suits<T, false>(n, k, device_cu_count());
         KAI_T(Q8_0) KAI_T(Q4_0) KAI_T(Q4_K) KAI_T(Q6_K) KAI_T(Q2_K) KAI_T(IQ3_S)
 #undef KAI_T
         default: return false;
@@ -56,11 +60,25 @@ void launch_mmq_decode(int type, const void *weight, int64_t n, int64_t k, int64
     }
 }
 
+// Whether up to MMQS_MAX_ROWS rows of this matrix run on the persistent GEMM over the image
+// (no partial sums) rather than the small-M GEMM.
+static bool image_persistent(int type, int64_t n, int64_t k) {
+    switch (type) {
+#define KAI_T(T) case T: return mmqd_suits<T, true>(n, k, device_cu_count());
+        KAI_T(Q8_0) KAI_T(Q4_0) KAI_T(Q4_K) KAI_T(Q6_K) KAI_T(Q2_K) KAI_T(IQ3_S)
+#undef KAI_T
+        default: return false;
+    }
+}
+
 void launch_mmq_planes(int type, const void *weight, int64_t n, int64_t k, int64_t m, const uint8_t *plane,
                        const float *inverse, float *partial, size_t partial_bytes, void *dst, bool dst_bf16,
                        int64_t stride_dst, hipStream_t stream, bool exact) {
+    const bool small = m <= MMQS_MAX_ROWS, persistent = small && image_persistent(type, n, k);
     if (exact && type == Q4_K) {  // the only format whose batched weight arithmetic rounds
-        if (m <= MMQS_MAX_ROWS)
+        if (persistent)
+            launch_mmqd_image<Q4_K, true>(weight, n, k, m, plane, inverse, dst, dst_bf16, stride_dst, stream);
+        else if (small)
             launch_mmqs<Q4_K, true>(weight, n, k, m, plane, inverse, partial, partial_bytes, dst, dst_bf16, stride_dst,
                                     stream);
         else
@@ -68,10 +86,13 @@ void launch_mmq_planes(int type, const void *weight, int64_t n, int64_t k, int64
         return;
     }
     if (exact && type != Q8_0 && type != Q6_K) throw Error("Exact batched arithmetic covers Q4_K, Q8_0 and Q6_K");
-    if (m <= MMQS_MAX_ROWS) {
+    if (small) {
         switch (type) {
 #define KAI_T(T) \
-    case T: launch_mmqs<T>(weight, n, k, m, plane, inverse, partial, partial_bytes, dst, dst_bf16, stride_dst, stream); return;
+    case T: \
+        if (persistent) launch_mmqd_image<T>(weight, n, k, m, plane, inverse, dst, dst_bf16, stride_dst, stream); \
+        else launch_mmqs<T>(weight, n, k, m, plane, inverse, partial, partial_bytes, dst, dst_bf16, stride_dst, stream); \
+        return;
             KAI_T(Q8_0) KAI_T(Q4_0) KAI_T(Q4_K) KAI_T(Q6_K) KAI_T(Q2_K) KAI_T(IQ3_S)
 #undef KAI_T
             default: throw Error("Unsupported fused MMQ weight type");
@@ -81,6 +102,7 @@ void launch_mmq_planes(int type, const void *weight, int64_t n, int64_t k, int64
 }
 
 size_t mmq_partial_bytes(int type, int64_t m, int64_t n, int64_t k) {
+    if (m <= MMQS_MAX_ROWS && image_persistent(type, n, k)) return 0;
     switch (type) {
 #define KAI_T(T) case T: return mmqs_partial_bytes<T>(m, n, k);
         KAI_T(Q8_0) KAI_T(Q4_0) KAI_T(Q4_K) KAI_T(Q6_K) KAI_T(Q2_K) KAI_T(IQ3_S)

@@ -16,4 +16,8 @@ template void launch_mmqs<Q4_K, true>(const void *, int64_t, int64_t, int64_t, c
                                       size_t, void *, bool, int64_t, hipStream_t);
 template void launch_mmqd<Q4_K>(const void *, int64_t, int64_t, int64_t, const block_q8_1 *, const float *, void *,
                              bool, int64_t, hipStream_t);
+template void launch_mmqd_image<Q4_K>(const void *, int64_t, int64_t, int64_t, const uint8_t *, const float *,
+                                    void *, bool, int64_t, hipStream_t);
+template void launch_mmqd_image<Q4_K, true>(const void *, int64_t, int64_t, int64_t, const uint8_t *,
+                                            const float *, void *, bool, int64_t, hipStream_t);
 }  // namespace kai

@@ -11,4 +11,6 @@ template void launch_mmqs<Q8_0>(const void *, int64_t, int64_t, int64_t, const u
                              size_t, void *, bool, int64_t, hipStream_t);
 template void launch_mmqd<Q8_0>(const void *, int64_t, int64_t, int64_t, const block_q8_1 *, const float *, void *,
                              bool, int64_t, hipStream_t);
+template void launch_mmqd_image<Q8_0>(const void *, int64_t, int64_t, int64_t, const uint8_t *, const float *,
+                                    void *, bool, int64_t, hipStream_t);
 }  // namespace kai
