@@ -60,16 +60,17 @@ def gemv_max_rows(qtype, k):  # kai_launch.h gemv_max_rows
     return {Q4_0: 8, Q8_0: 8, Q4_K: 4, Q6_K: 3 if k >= 12288 else 4, IQ3_S: 4, Q2_K: 3}[qtype]
 
 
-def persistent_decode(n, cus=256):
+def persistent(n, image=False, cus=256):
     """kai_mmqd.cuh mmqd_suits for the benched shapes (all fit its LDS): whole 16-row sets per
-    workgroup keep the workgroups busy for at least 90 % of the longest one's time."""
+    workgroup keep the workgroups busy for at least 90 % (85 % over the small-M image) of the
+    longest one's time."""
     sets = (n + 15) // 16
     wgs = min(sets, cus)
-    return sets * 10 >= 9 * wgs * -(-sets // wgs)
+    return sets * 20 >= (17 if image else 18) * wgs * -(-sets // wgs)
 
 
 def gemv_rows(qtype, n, k):  # kai_abi.hip run_decode
-    if persistent_decode(n):  # kai_launch.h gemv_rows_before_persistent
+    if persistent(n):  # kai_launch.h gemv_rows_before_persistent
         return {Q4_0: 6, Q8_0: 6, Q4_K: 3, Q2_K: 2}.get(qtype, gemv_max_rows(qtype, k))
     return gemv_max_rows(qtype, k)
 
@@ -96,10 +97,12 @@ def kernel_name(qtype, m, n, k):
     if m > 16:
         return "int8 MMQ (kai_fused_mmq_run: GGML MMQ planes + mmq_kernel)"
     if m > 8:
+        if persistent(n, image=True):
+            return "persistent int8 GEMM (kai_fused_mmq_run: GGML MMQ image + mmqd_kernel)"
         return "small-M int8 GEMM (kai_fused_mmq_run: GGML MMQ image + mmqs_kernel + reduction)"
     if m <= gemv_rows(qtype, n, k):
         return "v_dot4 GEMV (mmvq_kernel)"
-    if persistent_decode(n):
+    if persistent(n):
         return "persistent paired int8 GEMM (mmqd_kernel)"
     return "paired int8 MMQ tile (mmq_kernel, PAIR)"
 

@@ -336,12 +336,15 @@ inline MmqdSplit mmqd_split(int64_t n, int64_t k, int cus) {
 }
 // Whether an n x k matrix suits the persistent GEMM: the activation's K (decode: k % 256 == 0;
 // IMAGE: whole blocks of the type), a split that fits the LDS, and whole row sets per
-// workgroup keeping the workgroups busy for at least 90 % of the longest one's time (a
-// workgroup owns rowsets / wgs sets, rounded up or down). Measured on MI355X at 5 to 8 decode
-// rows against the tiled paired kernel: 2176 row sets (34816 x 5120: Q4_K 28.6 against 36.2
-// us, Q2_K 28.2 / 35.5, IQ3_S 42.9 / 54.8), 1024 (Q4_0 16384 x 2048, 15.0 / 24.5) and 128
+// workgroup keeping the workgroups busy for at least 90 % (IMAGE: 85 %) of the longest one's
+// time (a workgroup owns rowsets / wgs sets, rounded up or down). Measured on MI355X at 5 to 8
+// decode rows against the tiled paired kernel: 2176 row sets (34816 x 5120: Q4_K 28.6 against
+// 36.2 us, Q2_K 28.2 / 35.5, IQ3_S 42.9 / 54.8), 1024 (Q4_0 16384 x 2048, 15.0 / 24.5) and 128
 // (Q4_0 2048 x 8192, 15.7 / 30.0) gain; 448 (87.5 % busy: Q4_K 7168 x 5120, 12.8 / 12.1) and
-// 320 (62.5 %: Q6_K 5120 x 6144, 18.0 / 16.3) lose.
+// 320 (62.5 %: Q6_K 5120 x 6144, 18.0 / 16.3) lose. At 9 to 16 rows against the small-M GEMM
+// and its reduction (whole calls): 2176 row sets (Q4_K 41.0 / 37.8, Q2_K 51.0 / 48.6, IQ3_S
+// 55.6 / 52.8), 128 (Q8_0 2048 x 2048 28.0 / 13.4) and 448 (Q4_K 7168 x 5120 22.4 / 18.2) gain;
+// 320 (Q6_K 5120 x 6144 27.5 / 26.8, 5120 x 17408 38.7 / 68.8) does not.
 template <int TYPE, bool IMAGE>
 inline bool mmqd_suits(int64_t n, int64_t k, int cus) {
     const bool k_ok = IMAGE ? k >= MMQ_STEP / 8 && k % block_elems(TYPE) == 0 : k >= MMQ_STEP && k % MMQ_STEP == 0;
@@ -349,7 +352,7 @@ inline bool mmqd_suits(int64_t n, int64_t k, int cus) {
         n * ((k / block_elems(TYPE)) * block_bytes(TYPE)) >= (int64_t(1) << 32))
         return false;
     const int64_t rowsets = (n + 15) / 16, wgs = std::min<int64_t>(rowsets, cus), most = (rowsets + wgs - 1) / wgs;
-    return rowsets * 10 >= 9 * wgs * most && mmqd_split<TYPE, IMAGE>(n, k, cus).wgs > 0;
+    return rowsets * 20 >= (IMAGE ? 17 : 18) * wgs * most && mmqd_split<TYPE, IMAGE>(n, k, cus).wgs > 0;
 }
 
 template <int TYPE, bool IMAGE, bool EXACT>
