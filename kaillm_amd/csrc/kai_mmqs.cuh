@@ -338,12 +338,34 @@ static __global__ __launch_bounds__(256) void mmqs_reduce_kernel(const float *__
                                                                   int dst_bf16) {
     const int r = blockIdx.x, row = threadIdx.x / 16, c = 16 * r + threadIdx.x % 16;
     const int rowsets = (n + 15) / 16;
-    float s = 0.0f;
-    for (int ch = 0; ch < split.chunks; ++ch) {
+    auto pieces = [&](int ch, const float *&p) {
         const int sc = mmqs_chunk_steps(split, steps, ch), sce = mmqs_positions(sc), run = mmqs_run(split, rowsets, sc);
-        const int np = (r * sce + sce - 1) / run - (r * sce) / run + 1;
-        const float *p = partial + (int64_t(ch) * rowsets + r) * split.qmax * 256 + threadIdx.x;
-        for (int q = 0; q < np; ++q) s += p[q * 256];
+        p = partial + (int64_t(ch) * rowsets + r) * split.qmax * 256 + threadIdx.x;
+        return (r * sce + sce - 1) / run - (r * sce) / run + 1;
+    };
+    float s = 0.0f;
+    constexpr int MC = 4, MQ = 4;
+    if (split.chunks <= MC && split.qmax <= MQ) {  // every load in flight at once, then the same sums
+        float t[MC][MQ];
+        int np[MC];
+#pragma unroll
+        for (int ch = 0; ch < MC; ++ch) {
+            const float *p = partial;
+            np[ch] = ch < split.chunks ? pieces(ch, p) : 0;
+#pragma unroll
+            for (int q = 0; q < MQ; ++q) t[ch][q] = q < np[ch] ? p[q * 256] : 0.0f;
+        }
+#pragma unroll
+        for (int ch = 0; ch < MC; ++ch)
+#pragma unroll
+            for (int q = 0; q < MQ; ++q)
+                if (q < np[ch]) s += t[ch][q];
+    } else {
+        for (int ch = 0; ch < split.chunks; ++ch) {
+            const float *p;
+            const int np = pieces(ch, p);
+            for (int q = 0; q < np; ++q) s += p[q * 256];
+        }
     }
     if (row >= m || c >= n) return;  // rows past m hold zeros; columns past n are not stored
     const float v = s * inverse[row];
