@@ -344,6 +344,10 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
                     sl.back[t] |= (back < 16u ? back : 0u) << (4 * i);
                 }
             }
+        } else if constexpr (PAIR) {
+            const int s = min(it * KS + kg, steps - 1);  // past the end: the last step again
+#pragma unroll
+            for (int t = 0; t < TN; ++t) W::load(sl.raw[t], wrow[t] + int64_t(s) * W::SB, oct, 8);
         } else {
             const int s = it * KS + kg;
             if (s < steps) {
@@ -357,7 +361,7 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
     // writes and reads its own buffer, in order, so no barrier is needed).
     auto wfields = [&](const Slot &sl, typename W::Raw (&w)[TN], int it) {
         if constexpr (STREAM) {
-            const int nvalid = min(8, nb - 8 * (it * KS + kg));  // 32-value blocks of the step inside the row
+            const int nvalid = PAIR ? 8 : min(8, nb - 8 * (it * KS + kg));  // blocks of the step inside the row
 #pragma unroll
             for (int t = 0; t < TN; ++t) {
                 lds_u8 *tt = tbuf + t * mmq_tile_tbuf<TYPE>();
@@ -379,8 +383,10 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
         for (int t = 0; t < TN; ++t) acc[a][t] = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     const int aoct = W::act_pos(oct) / 8;  // octet of the activation block this lane multiplies
+    // PAIR: steps past the end (a k-group's last iteration, the ring's padding) multiply the
+    // last step's weights by a zero activation and add nothing.
     auto compute = [&](const Slot &sl, int buf, int it) {
-        if (it * KS + kg >= steps) return;  // wave-uniform
+        if (!PAIR && it * KS + kg >= steps) return;  // wave-uniform
         typename W::Raw w[TN];
         wfields(sl, w, it);
 #pragma unroll
@@ -468,18 +474,23 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
     // activation of step it+1 (loaded one iteration earlier) into the other buffer, load
     // the activation of step it+2, then the weights of step it+DEPTH. Vector loads retire
     // in order, so the wait for the activation of it+1 only covers weights that were
-    // already due; the far-ahead weight loads stay in flight across the barrier.
+    // already due; the far-ahead weight loads stay in flight across the barrier. PAIR: the
+    // loop runs whole turns of the ring (zero-activation steps pad the last) with no branch
+    // in its body, so the compiler's waits count the ring exactly.
     aload(0);
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) wload(wr[d], d);
     astore(0);
     aload(1);
     __syncthreads();
-    for (int it0 = 0; it0 < iters; it0 += DEPTH) {
+    const int end = PAIR ? (iters + DEPTH - 1) / DEPTH * DEPTH : iters;
+    for (int it0 = 0; it0 < end; it0 += DEPTH) {
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
             const int it = it0 + d;
-            if (it >= iters) break;
+            if constexpr (!PAIR) {
+                if (it >= iters) break;
+            }
             compute(wr[d], it & 1, it);
             astore((it + 1) & 1);
             aload(it + 2);
