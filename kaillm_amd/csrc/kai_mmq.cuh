@@ -562,11 +562,11 @@ static void launch_mmq_tile(const void *weight, int64_t n, int64_t k, const void
     const int64_t row_bytes = (k / block_elems(TYPE)) * block_bytes(TYPE);
     if (n * row_bytes >= (int64_t(1) << 32)) throw Error("MMQ takes matrices below 4 GiB");
     const size_t lds = mmq_lds_bytes<TYPE, TM, TN, KS>();
-    // weight steps in flight: one. The compiler drains every outstanding load before a
-    // step's compute (the loop's branches), so a deeper ring only costs registers and
-    // resident waves. Measured on MI355X: Q4_K gate/up at 8 rows 37.1 / 34.0 / 32.9 us with
-    // three / two / one steps; at 32-80 rows one against two steps, Q4_0 -5..-13 %, Q6_K
-    // and Q2_K unchanged.
+    // weight steps in flight: one. Measured on MI355X with one / two / three steps: the
+    // paired tile (whose loop has no branch, so its waits count the ring exactly) on Q6_K
+    // 5120x17408 at 8 rows 37.5 / 41.1 / 43.6 us, Q4_K 7168x5120 12.0 / 14.1 / 14.8 us; the
+    // tiled kernel at 32-80 rows one against two steps, Q4_0 -5..-13 %, Q6_K and Q2_K
+    // unchanged.
     constexpr int DEPTH = 1;
     auto kernel = mmq_kernel<TYPE, TM, TN, KS, DEPTH, PAIR, EXACT>;
     static DeviceFlags lds_raised;
