@@ -271,7 +271,10 @@ template <> struct MmqW<IQ3_S> {
 // instruction, and with superblocks of 210 bytes (Q6_K) that halves the achieved bandwidth.)
 template <int TYPE>
 struct MmqsStream {
-    static constexpr int SB = MmqW<TYPE>::SB, U = (SB + 15) / 16, SBP = 16 * U;
+    // row pitch: whole units, plus one when U is even, so that the 16 rows start on 16
+    // different 4-bank groups of the LDS (a pitch of 4U dwords with U even puts two rows on
+    // each group, and the lanes' field reads of a step conflict in pairs)
+    static constexpr int SB = MmqW<TYPE>::SB, U = (SB + 15) / 16, SBP = 16 * (U + (U % 2 == 0 ? 1 : 0));
     static constexpr int UPL = (16 * U + WAVE - 1) / WAVE;  // units per lane
 };
 

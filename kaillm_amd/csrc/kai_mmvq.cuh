@@ -73,7 +73,9 @@ inline size_t mmvq_act_lds_bytes(int64_t m, int64_t k, bool two_pass) {
 // +8 % and IQ3_S +25 %.
 template <int TYPE, int M, int G> constexpr bool gemv_streamed() { return TYPE == Q6_K && M == 1 && G >= 32; }
 template <int TYPE> struct GemvStream {
-    static constexpr int SB = block_bytes(TYPE), U = (SB + 15) / 16, SBP = 16 * U;
+    // superblock pitch: whole units, plus one when U is even (16 superblocks on 16 different
+    // 4-bank groups of the LDS, as in MmqsStream)
+    static constexpr int SB = block_bytes(TYPE), U = (SB + 15) / 16, SBP = 16 * (U + (U % 2 == 0 ? 1 : 0));
     static constexpr int UPL = (16 * U + WAVE - 1) / WAVE;  // units per lane
     static constexpr int BUF = 16 * SBP + 16;               // and a spare unit
 };
