@@ -85,33 +85,42 @@ template <int TYPE> struct GemvStream {
 // qkv / o_proj -2..-7 %; or three and four rows: 5120 x 17408 down -13..-16 %); 256
 // otherwise (two row sets: gate/up -8 % against 512; long rows at one or two activation
 // rows: down +10..17 % at 512); 128 from five rows on.
-template <int M, int RS, int G> constexpr int mmvq_threads() {
-    return M > 4 ? 128 : (RS == 1 && (G <= 16 || M >= 3)) ? 512 : 256;
+template <int M, int RS, int G, int KS = 1> constexpr int mmvq_threads() {
+    return M > 4 ? 128 : (KS > 1 || (RS == 1 && (G <= 16 || M >= 3))) ? 512 : 256;
 }
 
-template <int TYPE, int M, bool TWO_PASS, int DEPTH, int G, int RS>
-__global__ __launch_bounds__((mmvq_threads<M, RS, G>()))
+// KS > 1 (one row set per wave): the waves of a workgroup form groups of KS that share WAVE / G
+// rows, wave kp of a group taking the kp-th of KS equal parts of each row's units; the group's
+// totals are added in LDS in part order. It multiplies the resident waves of a matrix with few
+// rows without staging the activation more often.
+template <int TYPE, int M, bool TWO_PASS, int DEPTH, int G, int RS, int KS = 1>
+__global__ __launch_bounds__((mmvq_threads<M, RS, G, KS>()))
 void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrows, int units_per_row,
                  const block_q8_1 *__restrict__ y1, const block_q8_1 *__restrict__ y2, int y_row_blocks,
                  const float *__restrict__ inverse, void *__restrict__ dst, int64_t stride_dst, int dst_bf16) {
+    static_assert(KS == 1 || RS == 1, "a K split takes one row set per wave");
     using U = Unit<TYPE>;
-    constexpr int THREADS = mmvq_threads<M, RS, G>();
+    constexpr int THREADS = mmvq_threads<M, RS, G, KS>();
     constexpr int BYTES = block_bytes(TYPE);
     constexpr int PASSES = TWO_PASS ? 2 : 1;
     constexpr int ROWS = M * PASSES;  // activation rows staged
     extern __shared__ __align__(16) uint8_t kai_mmvq_lds[];
     __shared__ uint32_t grid_lds[TYPE == IQ3_S ? 512 : 1];
     __shared__ float inv_lds[M];
+    __shared__ float part_lds[KS > 1 ? (THREADS / WAVE / KS) * (KS - 1) * (WAVE / G) * M : 1];
 
     const int lane = threadIdx.x % WAVE;
     const int gpos = lane % G;
     // A wave owns RS row sets of WAVE / G consecutive rows, one group of G lanes per row,
     // streamed one after the other with the load ring running across their boundaries.
-    const int wave_row0 = (blockIdx.x * (THREADS / WAVE) + threadIdx.x / WAVE) * (WAVE / G) * RS;
+    const int wv = threadIdx.x / WAVE, kp = wv % KS, rg = wv / KS;  // K part and row group of the wave
+    const int wave_row0 = (blockIdx.x * (THREADS / WAVE / KS) + rg) * (WAVE / G) * RS;
     auto row_of = [&](int rs) { return wave_row0 + rs * (WAVE / G) + lane / G; };
     const int nb = y_row_blocks;
     const U unit = make_unit<TYPE>(gpos % U::PER_BLOCK, grid_lds);
     const int T = (units_per_row + G - 1) / G;
+    // the wave's steps of each row: [T0, T1) (all of them without a K split)
+    const int T0 = KS > 1 ? kp * T / KS : 0, T1 = KS > 1 ? (kp + 1) * T / KS : T;
 
     // Prime the ring first so the staging below overlaps the HBM latency. Every load is
     // unconditional (unit indices are clamped to the row, rows to the matrix, steps past
@@ -121,8 +130,8 @@ void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrow
     const int last = units_per_row - 1;
     // Step positions (row set, step within the set) advance by one per unit, uniformly.
     auto advance = [&](int &rs, int &tu) {
-        if (++tu == T) {
-            tu = 0;
+        if (++tu == T1) {
+            tu = T0;
             ++rs;
         }
     };
@@ -173,7 +182,7 @@ void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrow
         }
     };
     Slot ring[DEPTH];
-    int lrs = 0, ltu = 0;  // position of the next load
+    int lrs = 0, ltu = T0;  // position of the next load
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
         load_unit(ring[d], lrs, ltu);
@@ -213,7 +222,7 @@ void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrow
         }
         __syncthreads();
     }
-    if (wave_row0 >= nrows) return;  // whole wave past the last row
+    if (KS == 1 && wave_row0 >= nrows) return;  // whole wave past the last row (a K split meets a barrier below)
     // the wave's transpose buffer and the lane's superblock slot in it
     lds_u8 *tb = (lds_u8 *)kai_mmvq_lds + (size_t(ROWS) * nb * 40 + 15) / 16 * 16 + (threadIdx.x / WAVE) * S::BUF;
     const int jl = (lane / G) * (G / 4) + gpos / 4;
@@ -225,8 +234,8 @@ void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrow
     // T >= 1; a do-while keeps the prologue loads from being sunk behind a zero-trip check.
     // The memory clobbers keep each unit's loads where they are issued and the scheduling
     // barriers keep the next unit's arithmetic (and its load waits) out of this one.
-    const int TT = (RS * T + DEPTH - 1) / DEPTH * DEPTH;
-    int t0 = 0, rs = 0, tu = 0;  // position of the unit being multiplied
+    const int TT = (RS * (T1 - T0) + DEPTH - 1) / DEPTH * DEPTH;
+    int t0 = 0, rs = 0, tu = T0;  // position of the unit being multiplied
     do {
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
@@ -274,13 +283,28 @@ void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrow
     } while (t0 < TT);
 
     // Group totals of the last row set; lane gpos of a group stores activation rows
-    // j = gpos, gpos + G, ...
+    // j = gpos, gpos + G, ... (with a K split: part 0 after adding the other parts in order)
     const int row = row_of(RS - 1);
+    float total[M];
+#pragma unroll
+    for (int j = 0; j < M; ++j) total[j] = group_sum<G>(acc[j]);
+    if constexpr (KS > 1) {
+        float *part = part_lds + (rg * (KS - 1) * (WAVE / G) + lane / G) * M;  // [group][part - 1][row][j]
+        if (kp > 0 && gpos == 0) {
+#pragma unroll
+            for (int j = 0; j < M; ++j) part[(kp - 1) * (WAVE / G) * M + j] = total[j];
+        }
+        __syncthreads();
+        if (kp > 0) return;
+#pragma unroll
+        for (int p = 1; p < KS; ++p)
+#pragma unroll
+            for (int j = 0; j < M; ++j) total[j] += part[(p - 1) * (WAVE / G) * M + j];
+    }
 #pragma unroll
     for (int j = 0; j < M; ++j) {
-        const float total = group_sum<G>(acc[j]);
         if (gpos == j % G && row < nrows)
-            store_out(dst, dst_bf16 != 0, static_cast<int64_t>(j) * stride_dst + row, total * inv_lds[j]);
+            store_out(dst, dst_bf16 != 0, static_cast<int64_t>(j) * stride_dst + row, total[j] * inv_lds[j]);
     }
 }
 
@@ -298,10 +322,25 @@ inline int gemv_row_sets(int64_t n, int g) {
     return rows_ok && sets >= 2 * 4096 ? 2 : 1;
 }
 
-template <int TYPE, int M, bool TWO_PASS, int G, int RS>
+// K split (one row set per wave, three or four activation rows): waves sharing each row, so
+// that a matrix of few rows still puts 4 waves on every SIMD of a 256-CU device: 2 below 4096
+// waves, 4 below 2048, each part keeping at least two steps of its rows. Measured on MI355X
+// at three / four rows: Q6_K 5120x6144 14.4 / 16.2 -> 13.4 / 14.6 us, IQ3_S 5120x17408 27.8 /
+// 38.0 -> 25.2 / 36.4, Q4_0 2048x8192 at four rows 10.0 -> 9.1; Q2_K 5120x17408 at three rows
+// 26.0 -> 28.8 (not split); at one and two rows the 512-thread workgroups it needs cost more
+// than the waves gain (Q6_K 5120x17408 21.1 / 26.7 -> 25.0 / 28.1).
+template <int TYPE, int M>
+inline int gemv_k_split(int64_t n, int64_t k_units, int g) {
+    if (M < 3 || M > 4 || TYPE == Q2_K) return 1;
+    const int64_t waves = (n + (WAVE / g) - 1) / (WAVE / g), steps = (k_units + g - 1) / g;
+    const int ks = waves < 2048 ? 4 : waves < 4096 ? 2 : 1;
+    return steps >= 2 * ks ? ks : steps >= 4 ? 2 : 1;
+}
+
+template <int TYPE, int M, bool TWO_PASS, int G, int RS, int KS = 1>
 static void launch_sets(const uint8_t *w, int64_t n, int64_t k, const block_q8_1 *y1, const block_q8_1 *y2,
                         const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
-    constexpr int THREADS = mmvq_threads<M, RS, G>();
+    constexpr int THREADS = mmvq_threads<M, RS, G, KS>();
     // ring depth: one unit per lane in flight for the 256-value superblock formats with one
     // row set per wave; two with two row sets (whose next set's loads overlap the previous
     // set's reduction) and for the 32-value formats (one small block per unit). A deeper
@@ -314,14 +353,14 @@ static void launch_sets(const uint8_t *w, int64_t n, int64_t k, const block_q8_1
     const int64_t blocks_per_row = k / QK;
     const int64_t row_bytes = blocks_per_row * block_bytes(TYPE);
     const int units = static_cast<int>(blocks_per_row * Unit<TYPE>::PER_BLOCK);
-    const int64_t rows_per_block = (THREADS / WAVE) * (WAVE / G) * RS;
+    const int64_t rows_per_block = (THREADS / WAVE / KS) * (WAVE / G) * RS;
     constexpr bool STREAM = gemv_streamed<TYPE, M, G>();
     const size_t lds = (mmvq_act_lds_bytes(M, k, TWO_PASS) + 15) / 16 * 16 +
                        (STREAM ? size_t(THREADS / WAVE) * GemvStream<TYPE>::BUF : 0);
     if (lds + (TYPE == IQ3_S ? 2048 : 0) + 64 > size_t(MMVQ_LDS_BUDGET))
         throw Error("GEMV activation does not fit in LDS (m * k too large)");
     if (STREAM && (n + 64) * row_bytes >= (int64_t(1) << 32)) throw Error("The GEMV takes matrices below 4 GiB");
-    auto kernel = mmvq_kernel<TYPE, M, TWO_PASS, DEPTH, G, RS>;
+    auto kernel = mmvq_kernel<TYPE, M, TWO_PASS, DEPTH, G, RS, KS>;
     static DeviceFlags lds_raised;  // per instantiation and device
     raise_dynamic_lds(reinterpret_cast<const void *>(kernel), MMVQ_LDS_BUDGET - 4096, lds_raised,
                       "Cannot raise the GEMV dynamic LDS limit");
@@ -337,6 +376,11 @@ static void launch_variant(const uint8_t *w, int64_t n, int64_t k, const block_q
         if (gemv_row_sets<TYPE, M>(n, G) == 2) {
             launch_sets<TYPE, M, TWO_PASS, G, 2>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream);
             return;
+        }
+        switch (gemv_k_split<TYPE, M>(n, (k / block_elems(TYPE)) * Unit<TYPE>::PER_BLOCK, G)) {
+            case 4: launch_sets<TYPE, M, TWO_PASS, G, 1, 4>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream); return;
+            case 2: launch_sets<TYPE, M, TWO_PASS, G, 1, 2>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream); return;
+            default: break;
         }
     }
     launch_sets<TYPE, M, TWO_PASS, G, 1>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream);
