@@ -86,7 +86,7 @@ template <int TYPE> struct GemvStream {
 // otherwise (two row sets: gate/up -8 % against 512; long rows at one or two activation
 // rows: down +10..17 % at 512); 128 from five rows on.
 template <int M, int RS, int G, int KS = 1> constexpr int mmvq_threads() {
-    return M > 4 ? 128 : (KS > 1 || (RS == 1 && (G <= 16 || M >= 3))) ? 512 : 256;
+    return M > 4 ? 128 : ((KS > 1 && M >= 3) || (RS == 1 && (G <= 16 || M >= 3))) ? 512 : 256;
 }
 
 // KS > 1 (one row set per wave): the waves of a workgroup form groups of KS that share WAVE / G
@@ -322,16 +322,18 @@ inline int gemv_row_sets(int64_t n, int g) {
     return rows_ok && sets >= 2 * 4096 ? 2 : 1;
 }
 
-// K split (one row set per wave, three or four activation rows): waves sharing each row, so
-// that a matrix of few rows still puts 4 waves on every SIMD of a 256-CU device: 2 below 4096
-// waves, 4 below 2048, each part keeping at least two steps of its rows. Measured on MI355X
-// at three / four rows: Q6_K 5120x6144 14.4 / 16.2 -> 13.4 / 14.6 us, IQ3_S 5120x17408 27.8 /
-// 38.0 -> 25.2 / 36.4, Q4_0 2048x8192 at four rows 10.0 -> 9.1; Q2_K 5120x17408 at three rows
-// 26.0 -> 28.8 (not split); at one and two rows the 512-thread workgroups it needs cost more
-// than the waves gain (Q6_K 5120x17408 21.1 / 26.7 -> 25.0 / 28.1).
+// K split (one row set per wave): waves sharing each row, so that a matrix of few rows still
+// puts 4 waves on every SIMD of a 256-CU device: 2 below 4096 waves, 4 below 2048, each part
+// keeping at least two steps of its rows; 512-thread workgroups at three and four activation
+// rows, 256 at one and two. Measured on MI355X: at three / four rows Q6_K 5120x6144 14.4 / 16.2
+// -> 13.4 / 14.6 us, IQ3_S 5120x17408 27.8 / 38.0 -> 24.7 / 35.8, Q4_0 2048x8192 at four rows
+// 9.8 -> 9.0, but Q2_K 5120x17408 at three rows 26.0 -> 28.8; at one / two rows Q2_K
+// 5120x17408 14.7 / 20.3 -> 13.0 / 19.0, but Q6_K 5120x17408 21.2 / 26.9 -> 23.3 / 32.2 and
+// 5120x6144 10.8 / 12.3 -> 11.6 / 13.1. So Q2_K splits at one and two rows, the other formats
+// at three and four.
 template <int TYPE, int M>
 inline int gemv_k_split(int64_t n, int64_t k_units, int g) {
-    if (M < 3 || M > 4 || TYPE == Q2_K) return 1;
+    if (M > 4 || (TYPE == Q2_K) != (M <= 2)) return 1;
     const int64_t waves = (n + (WAVE / g) - 1) / (WAVE / g), steps = (k_units + g - 1) / g;
     const int ks = waves < 2048 ? 4 : waves < 4096 ? 2 : 1;
     return steps >= 2 * ks ? ks : steps >= 4 ? 2 : 1;
