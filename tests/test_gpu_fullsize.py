@@ -25,8 +25,9 @@ def quantized(qtype, n, k, rng):
     return quantize((rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)), qtype)
 
 
-# GEMV (kai_fused_mmvq) at 34816 x 5120: two row sets per wave for Q4_K at 1-4 rows and for
-# the other formats at 3-4 rows, up to each format's GEMV row limit (larger m goes to MMQ).
+# kai_fused_mmvq at 34816 x 5120: the GEMV's two row sets per wave for Q4_K at 1-3 rows and
+# the other formats at 3-4 rows; above the GEMV's rows on this matrix (Q4_K at 4, Q2_K at 3)
+# the persistent paired GEMM.
 TWO_SETS = [(O.Q4_K, 2), (O.Q4_K, 3), (O.Q4_K, 4), (O.Q2_K, 3), (O.IQ3_S, 3), (O.IQ3_S, 4),
             (O.Q4_0, 3), (O.Q4_0, 4), (O.Q8_0, 3), (O.Q8_0, 4), (O.Q6_K, 3), (O.Q6_K, 4)]
 
@@ -36,6 +37,26 @@ def test_gemv_two_row_sets(kai, qtype, m):
     n, k = 34816, 5120
     print(f"gemv two row sets {O.NAMES[qtype]} {n}x{k} m={m}", flush=True)
     rng = np.random.default_rng(qtype * 10 + m)
+    w = O.random_blocks(qtype, n, k, rng)
+    x = rng.standard_normal((m, k), dtype=np.float32).astype(np.float16)
+    out = gpu_mmvq(kai, qtype, to_dev(w), n, k, gpu_prepare(kai, to_dev(x)), m)
+    cols = sample_cols(n, rng)
+    ref = O.mul_mat(qtype, w[cols], k, O.prepare(x), m, threads=16)
+    err = O.normwise_rel(out[:, cols].cpu().numpy(), ref)
+    print(f"  normwise rel err {err:.3e}")
+    assert err <= TOL_F32
+
+
+# GEMV with K split (waves sharing each row): Q2_K at one and two rows, the other formats at
+# three and four, on matrices of few rows (kai_mmvq.cuh gemv_k_split: 2 or 4 parts).
+K_SPLIT = [(O.Q2_K, 5120, 17408, 1), (O.Q2_K, 5120, 17408, 2), (O.Q6_K, 5120, 6144, 3), (O.Q6_K, 5120, 6144, 4),
+           (O.IQ3_S, 5120, 17408, 3), (O.Q4_0, 2048, 8192, 4), (O.Q8_0, 2048, 2048, 3), (O.Q4_K, 7168, 5120, 4)]
+
+
+@pytest.mark.parametrize("qtype,n,k,m", K_SPLIT, ids=[f"{O.NAMES[t]}-{n}x{k}-m{m}" for t, n, k, m in K_SPLIT])
+def test_gemv_k_split(kai, qtype, n, k, m):
+    print(f"gemv k split {O.NAMES[qtype]} {n}x{k} m={m}", flush=True)
+    rng = np.random.default_rng(qtype * 100 + m)
     w = O.random_blocks(qtype, n, k, rng)
     x = rng.standard_normal((m, k), dtype=np.float32).astype(np.float16)
     out = gpu_mmvq(kai, qtype, to_dev(w), n, k, gpu_prepare(kai, to_dev(x)), m)
