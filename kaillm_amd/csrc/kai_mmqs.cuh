@@ -328,9 +328,11 @@ __global__ __launch_bounds__(WAVES * WAVE) void mmqs_kernel(
 // out[row][c] = inverse[row] * sum over chunks, then pieces (in order), of the partial sums
 // of c's row set. One workgroup per row set: thread t adds output (row t / 16, column
 // 16 r + t % 16), so each piece's 16 x 16 sums are one contiguous KiB read by one load and the
-// piece counts are uniform. (Combining the pieces in the GEMM itself, by the last wave to
-// finish a row set, needs an agent-scope release and acquire per wave: on MI355X those write
-// back and invalidate the XCD's L2 and made the GEMM six times slower.)
+// piece counts are uniform. (Combining the pieces in the GEMM itself needs an agent-scope
+// release and acquire, which on MI355X write back and invalidate the XCD's L2: per wave and
+// piece they made the GEMM six times slower; once per workgroup after its run, with per-row-set
+// piece counters in the scratch, the call took 24 to 39 % longer than with this launch at 9
+// and 16 rows on 5120 x 17408 and 5120 x 6144.)
 static __global__ __launch_bounds__(256) void mmqs_reduce_kernel(const float *__restrict__ partial, MmqsSplit split,
                                                                   int steps, int m, int n,
                                                                   const float *__restrict__ inverse,
