@@ -92,34 +92,79 @@ __device__ __forceinline__ float quad_sum(float v) {
     return v + dpp_f32<DPP_QUAD_2301>(v);
 }
 
-// Scale of a row from its maximum |x|, read by every workgroup of the row.
-// The row is read in runs of 8 values, run p by thread p % PREP_THREADS; the run this
-// workgroup's thread quantises (blockIdx.y * PREP_THREADS + threadIdx.x: 4 lanes per
-// block, PREP_BLOCKS blocks per workgroup) is kept in `own`, so the values are read once
-// (when that run is past the row end the thread stores nothing).
+// 8 consecutive source values as loaded (two float4 for fp32, one uint4 of 16-bit values),
+// and their conversion to float (load8 split in two, so loads can be issued back to back).
 template <int DTYPE>
-__device__ __forceinline__ float row_scale(const typename Src<DTYPE>::T *xr, int k, float *lds, float *inverse_out,
-                                           bool writer, float (&own)[8]) {
+struct Raw8 {
+    uint4 a, b;  // b unused for 16-bit sources
+};
+template <int DTYPE>
+__device__ __forceinline__ void load_raw8(const typename Src<DTYPE>::T *p, Raw8<DTYPE> &r) {
+    if constexpr (DTYPE == 0) {
+        r.a = load_unaligned<uint4>(p);
+        r.b = load_unaligned<uint4>(p + 4);
+    } else {
+        r.a = load_unaligned<uint4>(p);
+    }
+}
+template <int DTYPE>
+__device__ __forceinline__ void convert8(const Raw8<DTYPE> &r, float (&v)[8]) {
+    const uint32_t w[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+    if constexpr (DTYPE == 0) {
+        const uint32_t x[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = __builtin_bit_cast(float, w[i]);
+            v[4 + i] = __builtin_bit_cast(float, x[i]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = DTYPE == 1 ? bf16_bits_to_float(w[i] & 0xffffu) : half_bits_to_float(w[i] & 0xffffu);
+            v[2 * i + 1] = DTYPE == 1 ? bf16_bits_to_float(w[i] >> 16) : half_bits_to_float(w[i] >> 16);
+        }
+    }
+}
+
+// Maximum |x| of the thread's runs of a row (run p by thread p % PREP_THREADS), ROUND runs
+// at a time: the round's loads are issued back to back (indices clamped to the last run,
+// whose values are then ignored) before the first maximum. The run with index
+// blockIdx.y * PREP_THREADS + threadIdx.x is kept in `own`.
+template <int DTYPE, int ROUND>
+__device__ __forceinline__ float row_max(const typename Src<DTYPE>::T *xr, int runs, float (&own)[8]) {
     float mx = 0.0f;
-    const int runs = k / 8;
-    // Four runs per round, loaded unconditionally (indices clamped to the last run, whose
-    // values are then ignored) so that they are all in flight before the first maximum.
-    for (int i0 = 0; i0 * PREP_THREADS < runs; i0 += 4) {
-        float v[4][8];
+    for (int i0 = 0; i0 * PREP_THREADS < runs; i0 += ROUND) {
+        Raw8<DTYPE> r[ROUND];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) load8<DTYPE>(xr + 8 * min(int(threadIdx.x) + (i0 + u) * PREP_THREADS, runs - 1), v[u]);
+        for (int u = 0; u < ROUND; ++u)
+            load_raw8<DTYPE>(xr + 8 * min(int(threadIdx.x) + (i0 + u) * PREP_THREADS, runs - 1), r[u]);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < ROUND; ++u) {
+            float v[8];
+            convert8<DTYPE>(r[u], v);
             if (int(threadIdx.x) + (i0 + u) * PREP_THREADS < runs) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[u][j]));
+                for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[j]));
             }
             if (i0 + u == int(blockIdx.y)) {  // uniform
 #pragma unroll
-                for (int j = 0; j < 8; ++j) own[j] = v[u][j];
+                for (int j = 0; j < 8; ++j) own[j] = v[j];
             }
         }
     }
+    return mx;
+}
+
+// Scale of a row from its maximum |x|, read by every workgroup of the row. The run this
+// workgroup's thread quantises (blockIdx.y * PREP_THREADS + threadIdx.x: 4 lanes per block,
+// PREP_BLOCKS blocks per workgroup) is kept in `own`, so the values are read once (when that
+// run is past the row end the thread stores nothing). Rows of up to 8192 values take one
+// round of 4 runs per thread; longer rows rounds of 12 (one wait on memory up to 24576).
+template <int DTYPE>
+__device__ __forceinline__ float row_scale(const typename Src<DTYPE>::T *xr, int k, float *lds, float *inverse_out,
+                                           bool writer, float (&own)[8]) {
+    const int runs = k / 8;
+    const float mx = runs <= 4 * PREP_THREADS ? row_max<DTYPE, 4>(xr, runs, own) : row_max<DTYPE, 12>(xr, runs, own);
     return row_scale_from_max(block_max(mx, lds), inverse_out, writer);
 }
 static_assert(PREP_THREADS == 4 * PREP_BLOCKS, "one run of 8 values per thread and workgroup");
