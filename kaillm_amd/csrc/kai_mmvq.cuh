@@ -200,15 +200,28 @@ void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrow
     uint8_t *act = kai_mmvq_lds;
     uint32_t *sums = reinterpret_cast<uint32_t *>(kai_mmvq_lds + size_t(ROWS) * nb * 36);
     {
+        // 16-byte vectors by direct global-to-LDS copies where both ends are 16-byte aligned
+        // (a wave's 64 lanes fill 1 KiB in lane order), all in flight at once: copied through
+        // registers, each round of vectors waited for the previous one (and for the ring's
+        // loads, issued before them)
         const int pass_bytes = M * nb * 36;
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const uint8_t *src = reinterpret_cast<const uint8_t *>(p ? y2 : y1);
             uint8_t *dstl = act + p * pass_bytes;
             const int vec = pass_bytes / 16;
-            for (int i = threadIdx.x; i < vec; i += THREADS) {
-                const uint4 v = load_unaligned<uint4>(src + 16 * i);  // 4-byte aligned runs
-                __builtin_memcpy(dstl + 16 * i, &v, 16);
+            if ((reinterpret_cast<uintptr_t>(src) & 15) == 0 && (p * pass_bytes) % 16 == 0) {  // uniform
+                for (int i0 = (threadIdx.x / WAVE) * WAVE; i0 < vec; i0 += THREADS) {
+                    if (i0 + lane < vec)
+                        __builtin_amdgcn_global_load_lds(static_cast<const void *>(src + 16 * (i0 + lane)),
+                                                         (__attribute__((address_space(3))) uint8_t *)dstl + 16 * i0,
+                                                         16, 0, 0);
+                }
+            } else {
+                for (int i = threadIdx.x; i < vec; i += THREADS) {
+                    const uint4 v = load_unaligned<uint4>(src + 16 * i);  // 4-byte aligned runs
+                    __builtin_memcpy(dstl + 16 * i, &v, 16);
+                }
             }
             for (int i = 4 * vec + threadIdx.x; i < pass_bytes / 4; i += THREADS)
                 reinterpret_cast<uint32_t *>(dstl)[i] = reinterpret_cast<const uint32_t *>(src)[i];
