@@ -179,8 +179,10 @@ __global__ __launch_bounds__(WAVES * WAVE) void mmqs_kernel(
     const int chunk_id = blockIdx.x / split.wgs;
     const int s0 = chunk_id * split.chunk, sc = mmqs_chunk_steps(split, steps, chunk_id);
     const int rowsets = (n + 15) / 16;
-    // this wave's run [t0, t1) of the chunk's (row set, step) sequence
-    const int w = (blockIdx.x % split.wgs) * WAVES + wave;
+    // this wave's run [t0, t1) of the chunk's (row set, step) sequence. Runs are dealt to the
+    // chunk's workgroups in turn (run w to wave w / wgs of workgroup w % wgs), so that when a
+    // chunk has fewer runs than waves every workgroup, and so every CU, still gets a share.
+    const int w = wave * split.wgs + blockIdx.x % split.wgs;
     const int sce = mmqs_positions(sc), run = mmqs_run(split, rowsets, sc), total = rowsets * sce;
     const int t0 = w < split.waves ? min(w * run, total) : total, t1 = w < split.waves ? min(t0 + run, total) : total;
     if constexpr (TYPE == IQ3_S) {
