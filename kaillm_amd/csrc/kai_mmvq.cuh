@@ -340,13 +340,23 @@ inline int gemv_row_sets(int64_t n, int g) {
 // keeping at least two steps of its rows; 512-thread workgroups at three and four activation
 // rows, 256 at one and two. Measured on MI355X: at three / four rows Q6_K 5120x6144 14.4 / 16.2
 // -> 13.4 / 14.6 us, IQ3_S 5120x17408 27.8 / 38.0 -> 24.7 / 35.8, Q4_0 2048x8192 at four rows
-// 9.8 -> 9.0, but Q2_K 5120x17408 at three rows 26.0 -> 28.8; at one / two rows Q2_K
-// 5120x17408 14.7 / 20.3 -> 13.0 / 19.0, but Q6_K 5120x17408 21.2 / 26.9 -> 23.3 / 32.2 and
-// 5120x6144 10.8 / 12.3 -> 11.6 / 13.1. So Q2_K splits at one and two rows, the other formats
-// at three and four.
+// 9.8 -> 9.0, but Q2_K 5120x17408 at three rows 26.0 -> 28.8; at one / two rows (whole calls
+// with the preparation) Q2_K 5120x17408 14.7 / 20.3 -> 13.0 / 19.0, Q4_K 7168x5120 9.88 / 10.58
+// -> 9.49 / 10.80, Q4_0 3072x2048 7.89 / 8.01 -> 7.00 / 7.20, Q4_0 2048x8192 8.58 / 9.43 -> 8.34 /
+// 9.86, but Q6_K 5120x17408 22.97 / 27.98 -> 24.43 / 31.26 and 5120x6144 14.18 / 14.65 -> 14.86 /
+// 16.10. So Q2_K splits at one and two rows; Q4_K, Q4_0 and Q8_0 at one row, and Q4_0 and Q8_0
+// at two rows on rows of at most 2048 values; every other format at three and four.
 template <int TYPE, int M>
-inline int gemv_k_split(int64_t n, int64_t k_units, int g) {
-    if (M > 4 || (TYPE == Q2_K) != (M <= 2)) return 1;
+constexpr bool gemv_k_split_rows(int64_t k) {
+    if (M >= 3 && M <= 4) return TYPE != Q2_K;
+    if (TYPE == Q2_K) return M <= 2;
+    if (M == 1) return TYPE == Q4_K || TYPE == Q4_0 || TYPE == Q8_0;
+    return M == 2 && (TYPE == Q4_0 || TYPE == Q8_0) && k <= 2048;
+}
+template <int TYPE, int M>
+inline int gemv_k_split(int64_t n, int64_t k, int g) {
+    if (!gemv_k_split_rows<TYPE, M>(k)) return 1;
+    const int64_t k_units = (k / block_elems(TYPE)) * Unit<TYPE>::PER_BLOCK;
     const int64_t waves = (n + (WAVE / g) - 1) / (WAVE / g), steps = (k_units + g - 1) / g;
     const int ks = waves < 2048 ? 4 : waves < 4096 ? 2 : 1;
     return steps >= 2 * ks ? ks : steps >= 4 ? 2 : 1;
@@ -392,7 +402,7 @@ static void launch_variant(const uint8_t *w, int64_t n, int64_t k, const block_q
             launch_sets<TYPE, M, TWO_PASS, G, 2>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream);
             return;
         }
-        switch (gemv_k_split<TYPE, M>(n, (k / block_elems(TYPE)) * Unit<TYPE>::PER_BLOCK, G)) {
+        switch (gemv_k_split<TYPE, M>(n, k, G)) {
             case 4: launch_sets<TYPE, M, TWO_PASS, G, 1, 4>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream); return;
             case 2: launch_sets<TYPE, M, TWO_PASS, G, 1, 2>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream); return;
             default: break;
