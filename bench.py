@@ -71,6 +71,8 @@ def persistent(n, image=False, cus=256):
 
 def gemv_rows(qtype, n, k):  # kai_abi.hip run_decode
     if persistent(n):  # kai_launch.h gemv_rows_before_persistent
+        if qtype == Q4_0 and (n + 15) // 16 < 256:
+            return 8
         return {Q4_0: 6, Q8_0: 6, Q4_K: 3, Q2_K: 2}.get(qtype, gemv_max_rows(qtype, k))
     return gemv_max_rows(qtype, k)
 

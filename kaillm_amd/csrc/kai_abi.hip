@@ -120,7 +120,7 @@ void run_decode(int type, const void *weight, int64_t n, int64_t k, int64_t m, c
                 bool dst_bf16, int64_t stride_dst, hipStream_t s) {
     if (!l.y2 && k % 256 == 0) {
         const bool persistent = kai::mmq_decode_persistent(type, n, k);
-        const int gemv_rows = persistent ? kai::gemv_rows_before_persistent(type, k) : kai::gemv_max_rows(type, k);
+        const int gemv_rows = persistent ? kai::gemv_rows_before_persistent(type, k, n, kai::device_cu_count()) : kai::gemv_max_rows(type, k);
         if (m > gemv_rows || !kai::gemv_one_launch(m, k, 0)) {
             if (persistent) kai::launch_mmq_decode(type, weight, n, k, m, l.y1, l.inverse, dst, dst_bf16, stride_dst, s);
             else kai::launch_mmq(type, weight, n, k, m, l.y1, l.inverse, dst, dst_bf16, stride_dst, s);

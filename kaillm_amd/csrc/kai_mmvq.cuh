@@ -86,7 +86,7 @@ template <int TYPE> struct GemvStream {
 // otherwise (two row sets: gate/up -8 % against 512; long rows at one or two activation
 // rows: down +10..17 % at 512); 128 from five rows on.
 template <int M, int RS, int G, int KS = 1> constexpr int mmvq_threads() {
-    return M > 4 ? 128 : ((KS > 1 && M >= 3) || (RS == 1 && (G <= 16 || M >= 3))) ? 512 : 256;
+    return M > 4 ? (KS > 1 ? 512 : 128) : ((KS > 1 && M >= 3) || (RS == 1 && (G <= 16 || M >= 3))) ? 512 : 256;
 }
 
 // KS > 1 (one row set per wave): the waves of a workgroup form groups of KS that share WAVE / G
@@ -345,10 +345,13 @@ inline int gemv_row_sets(int64_t n, int g) {
 // -> 9.49 / 10.80, Q4_0 3072x2048 7.89 / 8.01 -> 7.00 / 7.20, Q4_0 2048x8192 8.58 / 9.43 -> 8.34 /
 // 9.86, but Q6_K 5120x17408 22.97 / 27.98 -> 24.43 / 31.26 and 5120x6144 14.18 / 14.65 -> 14.86 /
 // 16.10. So Q2_K splits at one and two rows; Q4_K, Q4_0 and Q8_0 at one row, and Q4_0 and Q8_0
-// at two rows on rows of at most 2048 values; every other format at three and four.
+// at two rows on rows of at most 2048 values; every other format at three and four; and Q4_0 at
+// five to eight rows, which the GEMV takes only on matrices of few rows
+// (gemv_rows_before_persistent), with 512-thread workgroups.
 template <int TYPE, int M>
 constexpr bool gemv_k_split_rows(int64_t k) {
-    if (M >= 3 && M <= 4) return TYPE != Q2_K;
+    if (M > 4) return M <= 8 && TYPE == Q4_0;
+    if (M >= 3) return TYPE != Q2_K;
     if (TYPE == Q2_K) return M <= 2;
     if (M == 1) return TYPE == Q4_K || TYPE == Q4_0 || TYPE == Q8_0;
     return M == 2 && (TYPE == Q4_0 || TYPE == Q8_0) && k <= 2048;
@@ -397,10 +400,12 @@ static void launch_sets(const uint8_t *w, int64_t n, int64_t k, const block_q8_1
 template <int TYPE, int M, bool TWO_PASS, int G>
 static void launch_variant(const uint8_t *w, int64_t n, int64_t k, const block_q8_1 *y1, const block_q8_1 *y2,
                            const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
-    if constexpr (M <= 4) {
-        if (gemv_row_sets<TYPE, M>(n, G) == 2) {
-            launch_sets<TYPE, M, TWO_PASS, G, 2>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream);
-            return;
+    if constexpr (M <= 4 || (M <= 8 && TYPE == Q4_0)) {
+        if constexpr (M <= 4) {
+            if (gemv_row_sets<TYPE, M>(n, G) == 2) {
+                launch_sets<TYPE, M, TWO_PASS, G, 2>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream);
+                return;
+            }
         }
         switch (gemv_k_split<TYPE, M>(n, k, G)) {
             case 4: launch_sets<TYPE, M, TWO_PASS, G, 1, 4>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream); return;

@@ -49,11 +49,12 @@ def test_gemv_two_row_sets(kai, qtype, m):
 
 # GEMV with K split (waves sharing each row) on matrices of few rows (kai_mmvq.cuh
 # gemv_k_split: 2 or 4 parts): Q2_K at one and two rows; Q4_K, Q4_0 and Q8_0 at one row, and
-# Q4_0 and Q8_0 at two rows on rows of at most 2048 values; the other formats at three and four.
+# Q4_0 and Q8_0 at two rows on rows of at most 2048 values; the other formats at three and four;
+# Q4_0 at five to eight rows on matrices of fewer 16-row sets than CUs.
 K_SPLIT = [(O.Q2_K, 5120, 17408, 1), (O.Q2_K, 5120, 17408, 2), (O.Q6_K, 5120, 6144, 3), (O.Q6_K, 5120, 6144, 4),
            (O.IQ3_S, 5120, 17408, 3), (O.Q4_0, 2048, 8192, 4), (O.Q8_0, 2048, 2048, 3), (O.Q4_K, 7168, 5120, 4),
            (O.Q4_K, 7168, 5120, 1), (O.Q4_0, 2048, 8192, 1), (O.Q4_0, 3072, 2048, 2), (O.Q8_0, 2048, 2048, 1),
-           (O.Q8_0, 2048, 2048, 2)]
+           (O.Q8_0, 2048, 2048, 2), (O.Q4_0, 2048, 8192, 8), (O.Q4_0, 3072, 2048, 5), (O.Q4_0, 3072, 2048, 7)]
 
 
 @pytest.mark.parametrize("qtype,n,k,m", K_SPLIT, ids=[f"{O.NAMES[t]}-{n}x{k}-m{m}" for t, n, k, m in K_SPLIT])
