@@ -12,8 +12,10 @@
 //     from the LDS image the preparation wrote (kai_launch.h, MmqPlanes), with direct
 //     global-to-LDS copies (global_load_lds_dwordx4): no registers, one barrier;
 //   * a chunk's work is the row-major sequence of (16-row set, K step) pairs; its waves take
-//     equal contiguous runs of it, so every SIMD gets the same number of steps whatever the
-//     shape. A run crosses row sets: the wave's ring of DEPTH steps of weight loads runs on
+//     equal contiguous runs of it (at least MMQS_MIN_RUN steps), so every SIMD gets the same
+//     number of steps whatever the shape; runs are dealt to the chunk's workgroups in turn, so
+//     a chunk with fewer runs than waves still reaches every CU. A run crosses row sets: the
+//     wave's ring of DEPTH steps of weight loads runs on
 //     across them, and at the end of each piece of a row set the wave stores its sums;
 //   * weights stream as contiguous 16-byte units per row into the wave's LDS transpose
 //     buffer (MmqsStream), from which each lane reads its MFMA operand fields;
