@@ -7,7 +7,7 @@
 // Design for gfx950. At 16 rows the whole product is a few tens of K steps per SIMD, so a
 // wave's start-up (its first weight loads from HBM) costs as much as its work unless each
 // wave starts once; the kernel is therefore persistent and stream-K balanced:
-//   * one workgroup of 16 waves per CU (MMQS_GRID of them); K is cut into as few chunks as
+//   * one workgroup of mmqs_waves waves per CU (MMQS_GRID of them); K is cut into as few chunks as
 //     the LDS holds (usually one), and each chunk's workgroups stage its activation once,
 //     from the LDS image the preparation wrote (kai_launch.h, MmqPlanes), with direct
 //     global-to-LDS copies (global_load_lds_dwordx4): no registers, one barrier;
@@ -32,7 +32,11 @@
 
 namespace kai {
 
-constexpr int MMQS_DEPTH = 2, MMQS_WAVES = 16;
+constexpr int MMQS_DEPTH = 2;
+// Waves per workgroup: 16, and 12 for IQ3_S. Measured on MI355X at 16 rows (whole calls), 12
+// against 16 waves: IQ3_S 5120x17408 36.70 -> 34.11 us, Q2_K 31.48 -> 31.28, Q6_K 5120x17408
+// 32.22 -> 32.11, but Q6_K 5120x6144 19.53 -> 20.62.
+template <int TYPE> constexpr int mmqs_waves() { return TYPE == IQ3_S ? 12 : 16; }
 constexpr int MMQS_GRID = 256;              // workgroups: one per CU of an MI355X
 constexpr int MMQS_LDS_BUDGET = 160 * 1024;  // the CU's LDS
 constexpr int MMQS_MIN_RUN = 4;             // K steps a wave takes at least (when it has work)
@@ -385,7 +389,7 @@ static __global__ __launch_bounds__(256) void mmqs_reduce_kernel(const float *__
 // steps. It depends only on the type and shape, so the scratch query and the launch agree.
 template <int TYPE>
 constexpr size_t mmqs_stream_lds() {  // per workgroup: 16 rows and a spare unit per wave
-    return size_t(MMQS_WAVES) * (16 * MmqsStream<TYPE>::SBP + 16);
+    return size_t(mmqs_waves<TYPE>()) * (16 * MmqsStream<TYPE>::SBP + 16);
 }
 template <int TYPE>
 inline MmqsSplit mmqs_split(int64_t n, int64_t k) {
@@ -400,7 +404,7 @@ inline MmqsSplit mmqs_split(int64_t n, int64_t k) {
     p.chunks = (steps + p.chunk - 1) / p.chunk;
     p.wgs = std::max(1, MMQS_GRID / p.chunks);
     const int64_t work = int64_t(rowsets) * mmqs_positions(p.chunk);  // the largest chunk's
-    p.waves = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(int64_t(p.wgs) * MMQS_WAVES,
+    p.waves = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(int64_t(p.wgs) * mmqs_waves<TYPE>(),
                                                                          work / MMQS_MIN_RUN)));
     p.qmax = 1;
     for (int c = 0; c < p.chunks; ++c) {
@@ -436,11 +440,11 @@ void launch_mmqs(const void *weight, int64_t n, int64_t k, int64_t m, const uint
     const int64_t row_bytes = (k / block_elems(TYPE)) * block_bytes(TYPE);
     if (n * row_bytes >= (int64_t(1) << 32)) throw Error("The small-M GEMM takes matrices below 4 GiB");
     const size_t lds = mmqs_lds_bytes<TYPE>(p);
-    auto kernel = mmqs_kernel<TYPE, MMQS_DEPTH, MMQS_WAVES, EXACT>;
+    auto kernel = mmqs_kernel<TYPE, MMQS_DEPTH, mmqs_waves<TYPE>(), EXACT>;
     static DeviceFlags lds_raised;
     raise_dynamic_lds(reinterpret_cast<const void *>(kernel), MMQS_LDS_BUDGET - (TYPE == IQ3_S ? 2048 : 0), lds_raised,
                       "Cannot raise the small-M GEMM's dynamic LDS limit");
-    kernel<<<dim3(static_cast<unsigned>(p.chunks * p.wgs)), MMQS_WAVES * WAVE, lds, stream>>>(
+    kernel<<<dim3(static_cast<unsigned>(p.chunks * p.wgs)), mmqs_waves<TYPE>() * WAVE, lds, stream>>>(
         static_cast<const uint8_t *>(weight), row_bytes, static_cast<int>(n), static_cast<int>(k), image,
         static_cast<int>(m), inverse, p, partial, dst, stride_dst, dst_bf16 ? 1 : 0);
     mmqs_reduce_kernel<<<static_cast<unsigned>((n + 15) / 16), 256, 0, stream>>>(
