@@ -39,8 +39,10 @@ INT8_PEAK_TOPS = 5000.0
 ROTATION_BYTES = 600e6   # weight copies per matrix: at least this many bytes in rotation
 MIN_COPIES = 3
 
-# BASELINE.json configs as (config, matrix, type, n, k, batches)
+# BASELINE.json configs as (config, matrix, type, n, k, batches). tests/test_gpu_bench_routes.py
+# generates its full-size oracle cases from these tables, so every timed route has a parity test.
 Q4_0, Q8_0, Q2_K, Q4_K, Q6_K, IQ3_S = 2, 8, 10, 12, 14, 21
+C3_BATCHES = (1, 2, 8, 16)
 C3 = [("gate_up", Q4_K, 34816, 5120), ("qkv", Q4_K, 7168, 5120), ("down", Q6_K, 5120, 17408),
       ("o_proj", Q6_K, 5120, 6144)]
 LEGS = [
@@ -82,7 +84,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=60)
     p.add_argument("--warmup", type=int, default=6)
-    p.add_argument("--batches", default="1,2,8,16")
+    p.add_argument("--batches", default=",".join(map(str, C3_BATCHES)))
     p.add_argument("--legs", default="all", help="'all', 'none', or a comma list of C1,C2,C3,C4,C5")
     p.add_argument("--reps", type=int, default=8, help="graph replays per leg")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")

@@ -61,11 +61,24 @@ class PackedGGUFLinear(torch.nn.Module):
         self.shape = (int(data.shape[0]), int(data.shape[1]) // block_bytes * qk)
         self.register_buffer("weight", data.detach().contiguous())
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        projection = native_fused.prepare([self])
+    def forward(self, x: torch.Tensor, bias: torch.Tensor | None = None, *,
+                output_dtype: torch.dtype | None = None) -> torch.Tensor:
+        """x @ W.T (+ bias) in output_dtype (the layer dtype, or FP32 for e.g. vocabulary
+        logits), with the reference's argument checks (``compact.py:364-394``)."""
+        if x.shape[-1] != self.shape[1]:
+            raise ValueError("GGUF activation width does not match the weight matrix")
+        if x.dtype != self.dtype or x.device != self.weight.device:
+            raise ValueError("GGUF activations and weights must share dtype and device")
+        output_dtype = self.dtype if output_dtype is None else output_dtype
+        if output_dtype not in (self.dtype, torch.float32):
+            raise ValueError("Compact GGUF output dtype must match activations or FP32")
+        projection = getattr(self, "_kai_fused", None)
+        if projection is None:
+            projection = native_fused.prepare([self]) or False
+            self._kai_fused = projection
         if not projection or not projection.supports(x):
             raise RuntimeError(f"the fused GGUF path cannot run x{tuple(x.shape)} {x.dtype} on {self.shape}")
-        return projection(x)
+        return _with_bias(projection(x, output_dtype), bias)
 
 
 def _with_bias(out, bias):

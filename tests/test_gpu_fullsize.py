@@ -84,41 +84,5 @@ def test_c2_qkv_decode(kai, m):
     assert O.normwise_rel(out.cpu().numpy(), ref) <= TOL_F32
 
 
-# The batched path (kai_fused_mmq_run) at every BASELINE shape above 8 rows: C3 batch 16,
-# C4 spec-verify (80) and prefill (512, 2048), C5 batch 16 and prefill.
-BATCHED = [
-    ("C3 Q4_K gate/up b16", O.Q4_K, 34816, 5120, 16),
-    ("C3 Q4_K qkv b16", O.Q4_K, 7168, 5120, 16),
-    ("C3 Q6_K down b16", O.Q6_K, 5120, 17408, 16),
-    ("C3 Q6_K o_proj b16", O.Q6_K, 5120, 6144, 16),
-    ("C4 Q4_K gate/up M80", O.Q4_K, 34816, 5120, 80),
-    ("C4 Q4_K down M80", O.Q4_K, 5120, 17408, 80),
-    ("C4 Q4_K gate/up M512", O.Q4_K, 34816, 5120, 512),
-    ("C4 Q4_K down M512", O.Q4_K, 5120, 17408, 512),
-    ("C4 Q4_K gate/up M2048", O.Q4_K, 34816, 5120, 2048),
-    ("C4 Q4_K down M2048", O.Q4_K, 5120, 17408, 2048),
-    ("C5 Q2_K gate/up b16", O.Q2_K, 34816, 5120, 16),
-    ("C5 Q2_K down b16", O.Q2_K, 5120, 17408, 16),
-    ("C5 Q2_K gate/up M2048", O.Q2_K, 34816, 5120, 2048),
-    ("C5 Q2_K down M2048", O.Q2_K, 5120, 17408, 2048),
-    ("C5 IQ3_S gate/up b16", O.IQ3_S, 34816, 5120, 16),
-    ("C5 IQ3_S down b16", O.IQ3_S, 5120, 17408, 16),
-    ("C5 IQ3_S gate/up M2048", O.IQ3_S, 34816, 5120, 2048),
-    ("C5 IQ3_S down M2048", O.IQ3_S, 5120, 17408, 2048),
-]
-
-
-@pytest.mark.parametrize("name,qtype,n,k,m", BATCHED, ids=[b[0] for b in BATCHED])
-def test_batched_full_size(kai, name, qtype, n, k, m):
-    print(f"batched full size {name}", flush=True)
-    rng = np.random.default_rng(n + k + m + qtype)
-    w = quantized(qtype, n, k, rng)
-    x = rng.standard_normal((m, k), dtype=np.float32).astype(np.float16)
-    out = gpu_mmq(kai, [(qtype, w, to_dev(w))], to_dev(x))
-    cols = sample_cols(n, rng)
-    got = out[:, torch.from_numpy(cols).to(out.device)].cpu().numpy()
-    del out
-    ref = O.mmq_reference(qtype, w[cols], x, threads=16)
-    err = O.normwise_rel(got, ref)
-    print(f"  normwise rel err {err:.3e}")
-    assert err <= TOL_F32
+# The batched path (kai_fused_mmq_run) at every BASELINE shape above 8 rows, like every
+# other leg the bench times, is in test_gpu_bench_routes.py (cases generated from bench.py).

@@ -161,3 +161,26 @@ def test_gguf_linear_method_unsharded_qweight(kai):
     y = GGUFLinearMethod().apply(layer, x)
     assert y.dtype == torch.float32
     assert O.normwise_rel(y.cpu().numpy(), _legacy_ref(O.Q2_K, w, x, 96)) <= 1e-3
+
+
+@pytest.mark.parametrize("m", [1, 5, 12, 40])
+def test_packed_linear_forward_bias_and_fp32_output(kai, m):
+    """PackedGGUFLinear(x, bias, output_dtype=torch.float32), the vocabulary role's FP32
+    logits (compact.py:364-407): the fused result in FP32 plus the bias, and in the layer
+    dtype by default."""
+    from kaillm_amd.linear import PackedGGUFLinear
+
+    print(f"PackedGGUFLinear.forward bias / fp32 m={m}", flush=True)
+    rng = np.random.default_rng(900 + m)
+    n, k = 136, 768
+    w = O.random_blocks(O.Q6_K, n, k, rng)
+    p = PackedGGUFLinear(to_dev(w), O.Q6_K, torch.bfloat16, role="vocabulary")
+    x_dev = to_dev(rng.standard_normal((m, k)).astype(np.float32)).to(torch.bfloat16)
+    ref = _ref(O.Q6_K, w, x_dev)
+    bias = torch.randn(n, device=DEV, dtype=torch.float32)
+    y32 = p(x_dev.reshape(1, m, k), bias, output_dtype=torch.float32)
+    assert y32.shape == (1, m, n) and y32.dtype == torch.float32
+    assert O.normwise_rel((y32 - bias).reshape(m, n).cpu().numpy(), ref) <= 1e-3
+    y16 = p(x_dev)
+    assert y16.dtype == torch.bfloat16 and y16.shape == (m, n)
+    assert O.normwise_rel(y16.float().cpu().numpy(), ref) <= TOL_BF16

@@ -81,3 +81,25 @@ def test_op_schemas_are_registered():
     # torch.library.custom_op types `int` arguments as SymInt, as for the reference's ops
     assert "(Tensor x, Tensor[] weights, SymInt[] types, SymInt[] rows_out, SymInt two_pass, bool out_f32)" in schema
     assert "SymInt a, SymInt b, SymInt s, bool out_f32" in str(torch.ops.kaillm.fused_mmvq_view.default._schema)
+
+
+def test_packed_linear_forward_checks_arguments():
+    """forward(x, bias=None, *, output_dtype=None) checks width, dtype/device and the output
+    dtype before running (compact.py:364-394); on the CPU the fused path then refuses."""
+    import inspect
+
+    from kaillm_amd.linear import PackedGGUFLinear
+
+    p = PackedGGUFLinear(_bytes(O.Q4_K, 8, 512), O.Q4_K, torch.bfloat16)
+    sig = inspect.signature(p.forward)
+    assert list(sig.parameters) == ["x", "bias", "output_dtype"]
+    assert sig.parameters["output_dtype"].kind is inspect.Parameter.KEYWORD_ONLY
+    with pytest.raises(ValueError, match="width does not match"):
+        p(torch.zeros((2, 256), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="share dtype and device"):
+        p(torch.zeros((2, 512), dtype=torch.float16))
+    with pytest.raises(ValueError, match="output dtype must match activations or FP32"):
+        p(torch.zeros((2, 512), dtype=torch.bfloat16), output_dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="fused GGUF path cannot run"):
+        p(torch.zeros((2, 512), dtype=torch.bfloat16), torch.zeros(8, dtype=torch.bfloat16),
+          output_dtype=torch.float32)
