@@ -104,8 +104,8 @@ size_t kai_ggml_a8_workspace(int type, int64_t row, int64_t k, int64_t vecs, int
  * half(sum x); Q4_K and Q2_K mins from d8 * sum q). Replaces ggml_mul_mat_vec_a8
  * (csrc/gguf/gguf_kernel.cu:104-218).
  * kai_ggml_mul_mat_a8 takes the legacy MMQ block dots, which differ only in Q4_K's min term
- * (the stored half(sum x)); every type but IQ3_S (the reference has no such kernel), and on
- * Q4_K, Q8_0 and Q6_K a multiple of four rows. Replaces ggml_mul_mat_a8
+ * (the stored half(sum x)); every type but IQ3_S (the reference has no such kernel), any row
+ * count. Replaces ggml_mul_mat_a8
  * (csrc/gguf/gguf_kernel.cu:220-290). */
 int kai_ggml_mul_mat_vec_a8(const void *weight, int type, int64_t row, const void *x, int x_dtype, int64_t vecs,
                             int64_t k, int64_t stride_x, void *y, int y_bf16, void *scratch, size_t scratch_bytes,

@@ -144,7 +144,6 @@ void legacy_check(int type, int64_t n, int64_t k, int64_t m, bool batched) {
     if (batched && type == kai::IQ3_S)
         throw kai::Error("ggml_mul_mat_a8 has no IQ3_S kernel (csrc/gguf/gguf_kernel.cu:229-288)");
     if (!shape_ok(type, n, k, 1, 1) || m < 1 || m > INT_MAX) throw kai::Error("Invalid legacy product shape");
-    if (legacy_on_planes(type, batched) && n % 4) throw kai::Error("ggml_mul_mat_a8 takes a multiple of four rows");
 }
 
 size_t legacy_scratch(int type, int64_t n, int64_t k, int64_t m, bool batched) {

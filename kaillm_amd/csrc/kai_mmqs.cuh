@@ -7,7 +7,7 @@
 // Design for gfx950. At 16 rows the whole product is a few tens of K steps per SIMD, so a
 // wave's start-up (its first weight loads from HBM) costs as much as its work unless each
 // wave starts once; the kernel is therefore persistent and stream-K balanced:
-//   * one workgroup of mmqs_waves waves per CU (MMQS_GRID of them); K is cut into as few chunks as
+//   * one workgroup of mmqs_waves waves per CU (at most MMQS_MAX_GRID); K is cut into as few chunks as
 //     the LDS holds (usually one), and each chunk's workgroups stage its activation once,
 //     from the LDS image the preparation wrote (kai_launch.h, MmqPlanes), with direct
 //     global-to-LDS copies (global_load_lds_dwordx4): no registers, one barrier;
@@ -37,7 +37,10 @@ constexpr int MMQS_DEPTH = 2;
 // against 16 waves: IQ3_S 5120x17408 36.70 -> 34.11 us, Q2_K 31.48 -> 31.28, Q6_K 5120x17408
 // 32.22 -> 32.11, but Q6_K 5120x6144 19.53 -> 20.62.
 template <int TYPE> constexpr int mmqs_waves() { return TYPE == IQ3_S ? 12 : 16; }
-constexpr int MMQS_GRID = 256;              // workgroups: one per CU of an MI355X
+// Workgroups: one per CU of the device, at most MMQS_MAX_GRID (an MI355X's 256 CUs). The
+// partial-sum scratch is sized for MMQS_MAX_GRID workgroups, which bounds it for any device:
+// fewer workgroups take longer runs and so cut every row set into fewer pieces.
+constexpr int MMQS_MAX_GRID = 256;
 constexpr int MMQS_LDS_BUDGET = 160 * 1024;  // the CU's LDS
 constexpr int MMQS_MIN_RUN = 4;             // K steps a wave takes at least (when it has work)
 
@@ -385,14 +388,14 @@ static __global__ __launch_bounds__(256) void mmqs_reduce_kernel(const float *__
 }
 
 // The split: K in as few chunks as the LDS holds (the staged chunk plus the waves' transpose
-// buffers), MMQS_GRID workgroups shared by the chunks, and runs of at least MMQS_MIN_RUN
-// steps. It depends only on the type and shape, so the scratch query and the launch agree.
+// buffers), `grid` workgroups shared by the chunks, and runs of at least MMQS_MIN_RUN steps.
+// It depends only on the type, the shape and the grid.
 template <int TYPE>
 constexpr size_t mmqs_stream_lds() {  // per workgroup: 16 rows and a spare unit per wave
     return size_t(mmqs_waves<TYPE>()) * (16 * MmqsStream<TYPE>::SBP + 16);
 }
 template <int TYPE>
-inline MmqsSplit mmqs_split(int64_t n, int64_t k) {
+inline MmqsSplit mmqs_split(int64_t n, int64_t k, int grid) {
     constexpr int BUF = mmqs_step_bytes<TYPE>();
     constexpr int MAX_CHUNK =  // even, so that an odd chunk's zero step fits too
         int((MMQS_LDS_BUDGET - mmqs_stream_lds<TYPE>() - (TYPE == IQ3_S ? 2048 : 0)) / BUF) / 2 * 2;
@@ -402,7 +405,7 @@ inline MmqsSplit mmqs_split(int64_t n, int64_t k) {
     p.chunks = (steps + MAX_CHUNK - 1) / MAX_CHUNK;
     p.chunk = (steps + p.chunks - 1) / p.chunks;
     p.chunks = (steps + p.chunk - 1) / p.chunk;
-    p.wgs = std::max(1, MMQS_GRID / p.chunks);
+    p.wgs = std::max(1, grid / p.chunks);
     const int64_t work = int64_t(rowsets) * mmqs_positions(p.chunk);  // the largest chunk's
     p.waves = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(int64_t(p.wgs) * mmqs_waves<TYPE>(),
                                                                          work / MMQS_MIN_RUN)));
@@ -418,12 +421,16 @@ inline size_t mmqs_lds_bytes(const MmqsSplit &p) {
     return size_t(mmqs_positions(p.chunk)) * mmqs_step_bytes<TYPE>() + mmqs_stream_lds<TYPE>();
 }
 
-// Partial-sum bytes of an m-row product with this matrix on the small-M GEMM.
+// Partial-sum bytes of a split (chunk, row set, piece, 16 x 16 fp32).
+inline size_t mmqs_split_bytes(const MmqsSplit &p, int64_t n) {
+    return size_t(p.chunks) * size_t((n + 15) / 16) * size_t(p.qmax) * 256 * sizeof(float);
+}
+// Partial-sum bytes of an m-row product with this matrix on the small-M GEMM, on any device
+// (the split of MMQS_MAX_GRID workgroups bounds every smaller grid's).
 template <int TYPE>
 inline size_t mmqs_partial_bytes(int64_t m, int64_t n, int64_t k) {
     if (m < 1 || m > MMQS_MAX_ROWS) return 0;
-    const MmqsSplit p = mmqs_split<TYPE>(n, k);
-    return size_t(p.chunks) * size_t((n + 15) / 16) * size_t(p.qmax) * 256 * sizeof(float);
+    return mmqs_split_bytes(mmqs_split<TYPE>(n, k, MMQS_MAX_GRID), n);
 }
 
 // image: the layout's small-M image (kai_launch.h) of the m activation rows. EXACT: the
@@ -434,8 +441,8 @@ void launch_mmqs(const void *weight, int64_t n, int64_t k, int64_t m, const uint
                  hipStream_t stream) {
     if (m < 1 || m > MMQS_MAX_ROWS) throw Error("The small-M GEMM takes 1..16 activation rows");
     if (n < 1 || k < MMQ_STEP / 8) throw Error("Invalid small-M GEMM shape");
-    const MmqsSplit p = mmqs_split<TYPE>(n, k);
-    const size_t need = mmqs_partial_bytes<TYPE>(m, n, k);
+    const MmqsSplit p = mmqs_split<TYPE>(n, k, std::min(device_cu_count(), MMQS_MAX_GRID));
+    const size_t need = mmqs_split_bytes(p, n);
     if (need > partial_bytes || !partial) throw Error("Scratch too small for the small-M GEMM's partial sums");
     const int64_t row_bytes = (k / block_elems(TYPE)) * block_bytes(TYPE);
     if (n * row_bytes >= (int64_t(1) << 32)) throw Error("The small-M GEMM takes matrices below 4 GiB");

@@ -321,22 +321,23 @@ void mmvq_kernel(const uint8_t *__restrict__ weight, int64_t row_bytes, int nrow
     }
 }
 
-// Row sets per wave: two when the matrix still gives at least 4096 waves (four per SIMD
-// of a 256-CU device) after pairing its row sets, for Q4_K at one to four activation rows
+// Row sets per wave: two when the matrix still gives at least four waves per SIMD of the
+// device (4096 on a 256-CU MI355X) after pairing its row sets, for Q4_K at one to four activation rows
 // and for the other formats at three or four; the second set's loads then overlap the
 // first set's reduction and the activation is staged once per twice the weight bytes.
 // Measured on MI355X, 34816 x 5120: Q4_K -11 %, -9 %, -14 %, -18 % at one to four rows;
 // Q2_K and IQ3_S -10 % to -22 % at three and four rows but +5 % at one; smaller matrices
 // lose parallelism and stay at one set.
 template <int TYPE, int M>
-inline int gemv_row_sets(int64_t n, int g) {
+inline int gemv_row_sets(int64_t n, int g, int cus) {
     const int64_t sets = (n + (WAVE / g) - 1) / (WAVE / g);
     const bool rows_ok = TYPE == Q4_K ? M <= 4 : (M >= 3 && M <= 4);
-    return rows_ok && sets >= 2 * 4096 ? 2 : 1;
+    return rows_ok && sets >= 2 * 16 * int64_t(cus) ? 2 : 1;
 }
 
 // K split (one row set per wave): waves sharing each row, so that a matrix of few rows still
-// puts 4 waves on every SIMD of a 256-CU device: 2 below 4096 waves, 4 below 2048, each part
+// puts 4 waves on every SIMD of the device: 2 below 16 waves per CU (4096 on a 256-CU
+// MI355X), 4 below 8 per CU, each part
 // keeping at least two steps of its rows; 512-thread workgroups at three and four activation
 // rows, 256 at one and two. Measured on MI355X: at three / four rows Q6_K 5120x6144 14.4 / 16.2
 // -> 13.4 / 14.6 us, IQ3_S 5120x17408 27.8 / 38.0 -> 24.7 / 35.8, Q4_0 2048x8192 at four rows
@@ -357,11 +358,11 @@ constexpr bool gemv_k_split_rows(int64_t k) {
     return M == 2 && (TYPE == Q4_0 || TYPE == Q8_0) && k <= 2048;
 }
 template <int TYPE, int M>
-inline int gemv_k_split(int64_t n, int64_t k, int g) {
+inline int gemv_k_split(int64_t n, int64_t k, int g, int cus) {
     if (!gemv_k_split_rows<TYPE, M>(k)) return 1;
     const int64_t k_units = (k / block_elems(TYPE)) * Unit<TYPE>::PER_BLOCK;
     const int64_t waves = (n + (WAVE / g) - 1) / (WAVE / g), steps = (k_units + g - 1) / g;
-    const int ks = waves < 2048 ? 4 : waves < 4096 ? 2 : 1;
+    const int ks = waves < 8 * int64_t(cus) ? 4 : waves < 16 * int64_t(cus) ? 2 : 1;
     return steps >= 2 * ks ? ks : steps >= 4 ? 2 : 1;
 }
 
@@ -402,12 +403,12 @@ static void launch_variant(const uint8_t *w, int64_t n, int64_t k, const block_q
                            const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
     if constexpr (M <= 4 || (M <= 8 && TYPE == Q4_0)) {
         if constexpr (M <= 4) {
-            if (gemv_row_sets<TYPE, M>(n, G) == 2) {
+            if (gemv_row_sets<TYPE, M>(n, G, device_cu_count()) == 2) {
                 launch_sets<TYPE, M, TWO_PASS, G, 2>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream);
                 return;
             }
         }
-        switch (gemv_k_split<TYPE, M>(n, k, G)) {
+        switch (gemv_k_split<TYPE, M>(n, k, G, device_cu_count())) {
             case 4: launch_sets<TYPE, M, TWO_PASS, G, 1, 4>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream); return;
             case 2: launch_sets<TYPE, M, TWO_PASS, G, 1, 2>(w, n, k, y1, y2, inverse, dst, dst_bf16, stride_dst, stream); return;
             default: break;

@@ -2,7 +2,7 @@
 
 A decode step of the fused path — the Gemma norm producer feeding a merged Q4_K/Q6_K
 projection, a SwiGLU down projection and a projection read through an input view — and
-the batched path (fp16-MFMA and int8 MMQ kernels with their scratch) are captured once,
+the batched path (the small-M, persistent and tiled GEMMs with their scratch) are captured once,
 then replayed with new inputs written into the captured buffers. Between replays the same
 step runs eagerly on the same inputs, and every replay must equal it bit for bit (the
 kernels have fixed reduction orders and no atomics). The library issues no memset and no

@@ -132,8 +132,8 @@ def test_legacy_ops_against_oracle(kai, qtype, m, dtype, batched):
 
 
 def test_legacy_gemm_shapes(kai):
-    """Row counts the planes route does not take (Q4_K needs four at a time); the decode
-    route takes any (Q4_0); K above 32768 dequantises."""
+    """Row counts that are not a multiple of four on the decode route (Q4_0) and the planes
+    route (Q4_K); K above 32768 dequantises."""
     from kaillm_amd.ops import ggml_mul_mat_a8, ggml_mul_mat_vec_a8
 
     rng = np.random.default_rng(3)
@@ -142,8 +142,8 @@ def test_legacy_gemm_shapes(kai):
     y = ggml_mul_mat_a8(to_dev(w), x, O.Q4_0, 66)
     assert O.normwise_rel(y.cpu().numpy(), O.legacy_reference(O.Q4_0, w, x.cpu().numpy(), 1)) <= TOL_F32
     w = _weights(O.Q4_K, 66, 256, rng, "quantized")
-    with pytest.raises(RuntimeError, match="multiple of four"):
-        ggml_mul_mat_a8(to_dev(w), x, O.Q4_K, 66)
+    y = ggml_mul_mat_a8(to_dev(w), x, O.Q4_K, 66)
+    assert O.normwise_rel(y.cpu().numpy(), O.legacy_reference(O.Q4_K, w, x.cpu().numpy(), 1)) <= TOL_F32
     assert O.normwise_rel(ggml_mul_mat_vec_a8(to_dev(w), x, O.Q4_K, 66).cpu().numpy(),
                           O.legacy_reference(O.Q4_K, w, x.cpu().numpy(), 0)) <= TOL_F32
     kk = 33024
@@ -151,6 +151,27 @@ def test_legacy_gemm_shapes(kai):
     xb = rng.standard_normal((2, kk)).astype(np.float32)
     y = ggml_mul_mat_vec_a8(to_dev(w), to_dev(xb), O.Q8_0, 16).cpu().numpy()
     assert O.normwise_rel(y, xb.astype(np.float64) @ O.dequantize(O.Q8_0, w, kk).astype(np.float64).T) <= 1e-5
+
+
+# ggml_mul_mat_a8 on the planes route (Q4_K, Q8_0, Q6_K) with row counts that are not a
+# multiple of four (an odd vocabulary, say), through every batched kernel: the small-M and
+# persistent GEMMs (9 and 16 rows) and the tiled one (17 and 40).
+@pytest.mark.parametrize("qtype", [O.Q4_K, O.Q8_0, O.Q6_K], ids=lambda t: O.NAMES[t])
+@pytest.mark.parametrize("n", [1, 67, 4099])
+@pytest.mark.parametrize("m", [9, 16, 17, 40])
+def test_legacy_gemm_ragged_rows(kai, qtype, n, m):
+    from kaillm_amd.ops import ggml_mul_mat_a8
+
+    print(f"legacy a8 ragged rows {O.NAMES[qtype]} n={n} m={m}", flush=True)
+    rng = np.random.default_rng(n + m + qtype)
+    k = 512
+    w = _weights(qtype, n, k, rng, "quantized")
+    x = to_dev(rng.standard_normal((m, k)).astype(np.float32))
+    y = ggml_mul_mat_a8(to_dev(w), x, qtype, n)
+    assert y.shape == (m, n)
+    err = O.normwise_rel(y.cpu().numpy(), O.legacy_reference(qtype, w, x.cpu().numpy(), 1))
+    print(f"  normwise rel err {err:.3e}")
+    assert err <= TOL_F32
 
 
 def test_legacy_iq3s_gemm_is_the_dequantising_route(kai):

@@ -61,6 +61,31 @@ def test_noalloc_equals_scratch_entry_on_two_calls(kai):
         assert O.normwise_rel(got.float().cpu().numpy(), ref) <= (2.0 ** -8 if bf16 else 1e-3)
 
 
+def test_noalloc_small_m_routes_after_a_larger_call(kai):
+    """Up to 16 rows the scratch holds the small-M image and, for matrices on the small-M GEMM,
+    its partial sums: a group with one matrix on each 9..16-row kernel (Q6_K 5120 x 5120: 320
+    row sets, the small-M GEMM and its reduction; Q4_K 7168 x 5120: 448 row sets, the
+    persistent GEMM over the image), at 16 and then 9 rows, right after an 80-row call that
+    filled the array with other bytes; bit for bit against kai_fused_mmq_run."""
+    rng = np.random.default_rng(99)
+    mats = []
+    k = 5120
+    for qtype, n in ((O.Q6_K, 5120), (O.Q4_K, 7168)):
+        w = O.random_blocks(qtype, n, k, rng)
+        mats.append((qtype, torch.from_numpy(w).to(DEV)))
+    big = torch.from_numpy(rng.standard_normal((80, k)).astype(np.float16)).to(DEV)
+    _run(kai, mats, big, noalloc=True)
+    for m in (16, 9):
+        print(f"noalloc small-M m={m}", flush=True)
+        x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float16)).to(DEV)
+        got = _run(kai, mats, x, noalloc=True)
+        want = _run(kai, mats, x, noalloc=False)
+        assert torch.equal(got, want)
+        ref = np.concatenate([O.mmq_reference(t, w.cpu().numpy(), x.cpu().numpy(), threads=16)
+                              for t, w in mats], axis=1)
+        assert O.normwise_rel(got.cpu().numpy(), ref) <= 1e-3
+
+
 def test_noalloc_refuses_beyond_capacity(kai):
     rng = np.random.default_rng(7)
     k, m = 17408, 2048   # 40 MiB of planes
