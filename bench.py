@@ -94,11 +94,15 @@ def parse():
                         "kernels of one C3 matrix on each weight copy, eager launches only")
     p.add_argument("--sample-matrix", default="gate_up", choices=[c[0] for c in C3],
                    help="the C3 matrix of --kernel-sample")
+    p.add_argument("--peaks", action="store_true",
+                   help="measure this device's ceilings instead (MFMA rate per kind, LDS reads, HBM copy)")
     return p.parse_args()
 
 
 def kernel_name(qtype, m, n, k):
     if m > 16:
+        if qtype in (Q4_K, Q4_0, Q8_0, IQ3_S, Q2_K) and (m > 96 or n <= 16384):  # kai_launch.h mmq_uses_h
+            return "fp16 folded-operand GEMM (kai_fused_mmq_run: fp16 image + mmqh_kernel)"
         return "int8 MMQ (kai_fused_mmq_run: GGML MMQ planes + mmq_kernel)"
     if m > 8:
         if persistent(n, image=True):
@@ -142,11 +146,17 @@ class Runner:
         if k not in self.act or self.act[k].numel() < self.lib.kai_fused_activation_bytes(8, k, 0):
             self.act[k] = torch.empty(self.lib.kai_fused_activation_bytes(8, k, 0), dtype=torch.uint8,
                                       device=self.dev)
-        if max_m > 8:
-            size = self.lib.kai_fused_mmq_workspace(0, self.groups[key][0][1], self.groups[key][0][2], 1, k, max_m, 1)
+
+    def workspace(self, key, k, m):
+        """The batched entry's scratch for this matrix at m rows (kai_fused_mmq_workspace per
+        shape, as a caller keeps it: its size is not monotonic in m, since split-K sums can make
+        a smaller product need more)."""
+        if (key, m) not in self.ws:
+            size = self.lib.kai_fused_mmq_workspace(0, self.groups[key][0][1], self.groups[key][0][2], 1, k, m, 1)
             if size == 0:
                 raise RuntimeError(self.lib.current_direct_error().decode())
-            self.ws[key] = torch.empty(size, dtype=torch.uint8, device=self.dev)
+            self.ws[(key, m)] = self.torch.empty(size, dtype=self.torch.uint8, device=self.dev)
+        return self.ws[(key, m)]
 
     def call(self, key, qtype, n, k, m, copy, s, prepare=True):
         """One projection: preparation + product (decode), or one batched call."""
@@ -159,7 +169,7 @@ class Runner:
                                                  self.act[k].data_ptr(), 0, self.out[n].data_ptr(), 0, n, s))
         else:
             ptrs, types, rows = self.groups[key][copy]
-            ws = self.ws[key]
+            ws = self.workspace(key, k, m)
             native.check(lib, lib.kai_fused_mmq_run(ptrs, types, rows, 1, x.data_ptr(), 2, k, k, m,
                                                     self.out[n].data_ptr(), 0, 0, ws.data_ptr(), ws.numel(), 0, s))
 
@@ -221,6 +231,9 @@ def main():
     batches = [int(b) for b in args.batches.split(",")]
     if args.kernel_sample:
         kernel_sample(lib, dev, batches, args.sample_matrix)
+        return
+    if args.peaks:
+        print(json.dumps(measure_peaks(lib, dev)), flush=True)
         return
     chosen = set(("C1,C2,C3,C4,C5" if args.legs == "all" else "" if args.legs == "none" else args.legs).split(","))
 
@@ -303,7 +316,8 @@ def main():
         for m in ms:
             leg(cfg, mname, qtype, n, k, m, key)
         del r.weights[key], r.groups[key]
-        r.ws.pop(key, None)
+        for wkey in [w for w in r.ws if w[0] == key]:
+            del r.ws[wkey]
         torch.cuda.empty_cache()
 
     cpu = None if args.no_cpu else cpu_baseline(r.weights[("C3", "gate_up")][0], Q4_K, 34816, 5120, args.cpu_seconds)
@@ -370,6 +384,68 @@ def kernel_sample(lib, dev, batches, matrix="gate_up"):
     torch.cuda.synchronize()
     print(f"[bench] kernel sample: 3 copies of {src.numel()} bytes, {matrix} {NAMES[qtype]} {n}x{k} x{MIN_COPIES} "
           f"at batch {batches}", flush=True)
+
+
+PEAK_KINDS = {0: "f16 v_mfma_f32_32x32x16_f16", 1: "f16 v_mfma_f32_16x16x32_f16", 2: "f16 v_mfma_f32_32x32x8_f16",
+              3: "int8 v_mfma_i32_32x32x32_i8", 4: "int8 v_mfma_i32_16x16x64_i8"}
+
+
+def measure_peaks(lib, dev):
+    """This device's ceilings, each kernel timed with HIP events on one stream (kai_peaks.h):
+    dense MFMA rate per instruction kind at one and at two waves per SIMD (4 independent
+    accumulation chains per wave), LDS read bandwidth, and a 2 GiB STREAM-style copy (bytes
+    read plus written)."""
+    import torch
+
+    from kaillm_amd import native
+
+    props = torch.cuda.get_device_properties(dev)
+    cus = props.multi_processor_count
+    s = torch.cuda.current_stream()
+    guard = torch.zeros(1024, dtype=torch.float32, device=dev)
+
+    def timed(fn, reps=5):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        best = float("inf")
+        for _ in range(reps):
+            e0.record(s)
+            fn()
+            e1.record(s)
+            torch.cuda.synchronize()
+            best = min(best, e0.elapsed_time(e1) * 1e-3)
+        return best
+
+    out = {"device": props.name, "cus": cus, "mfma": {}, "method": "best of 5 timed launches after one warm-up"}
+    iters = 20000
+    for kind, name in PEAK_KINDS.items():
+        ops = lib.kai_peak_mfma_ops(kind)
+        for threads in (256, 512):  # 1 and 2 waves per SIMD, one workgroup per CU
+            blocks = 4 * cus
+            t = timed(lambda: native.check(lib, lib.kai_peak_mfma(kind, iters, blocks, threads, guard.data_ptr(),
+                                                                  s.cuda_stream)))
+            tops = ops * 4 * iters * (threads // 64) * blocks / t / 1e12
+            out["mfma"][f"{name} ({threads // 256} wave/SIMD)"] = round(tops, 1)
+    lds_iters = 20000
+    blocks, threads = 4 * cus, 1024
+    t = timed(lambda: native.check(lib, lib.kai_peak_lds(lds_iters, blocks, threads, guard.data_ptr(),
+                                                         s.cuda_stream)))
+    lds_bytes = lds_iters * 4 * 16 * threads * blocks
+    out["lds_read_TBps"] = round(lds_bytes / t / 1e12, 2)
+    out["lds_read_bytes_per_cu_clk_at_2400MHz"] = round(lds_bytes / t / cus / 2.4e9, 1)
+    n = 1 << 31
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    best = {}
+    for blocks in (cus * 8, cus * 16, cus * 32):
+        t = timed(lambda: native.check(lib, lib.kai_peak_copy(src.data_ptr(), dst.data_ptr(), n, blocks,
+                                                              s.cuda_stream)))
+        best[blocks] = round(2 * n / t / 1e9, 1)
+    out["hbm_copy_GBps"] = max(best.values())
+    out["hbm_copy_by_grid"] = best
+    torch.cuda.synchronize()
+    return out
 
 
 def cpu_model():

@@ -66,24 +66,36 @@ Group validate_group(const int *types, const int64_t *rows, int count, int64_t k
 }
 
 // Scratch of one batched call, each region 256-aligned: [inverse: m fp32] then one plane
-// of GGML MMQ's activation (mmq_plane_bytes; up to 16 rows the small-M image) per layout a
-// matrix of the group reads, in the order D4, DS4, D2S6, then the small-M GEMM's partial
-// sums (the largest any matrix needs; the matrices use it in turn).
+// of GGML MMQ's activation (mmq_plane_bytes; up to 16 rows the small-M image) per layout that
+// a matrix on the int8 kernels reads, in the order D4, DS4, D2S6; then, above 16 rows, the
+// fp16 GEMM's image (codes, min-pass sums; kai_launch.h) per layout that a matrix on
+// it reads; then the partial sums (the small-M GEMM's, or the fp16 GEMM's split-K sums: the
+// largest any matrix needs; the matrices use them in turn). legacy: the legacy ops' call,
+// which reads the planes only.
 struct MmqScratch {
     size_t inverse = 0, plane[3] = {0, 0, 0}, partial = 0, partial_bytes = 0, total = 0;
-    bool has_plane[3] = {false, false, false};
+    size_t h_codes[3] = {0, 0, 0}, h_mins[3] = {0, 0, 0};
+    bool has_plane[3] = {false, false, false}, has_h[3] = {false, false, false};
 };
-MmqScratch mmq_scratch(const int *types, const int64_t *rows, int count, int64_t k, int64_t m) {
+MmqScratch mmq_scratch(const int *types, const int64_t *rows, int count, int64_t k, int64_t m, bool legacy = false) {
     MmqScratch p;
     for (int i = 0; i < count; ++i) {
-        p.has_plane[kai::mmq_layout(types[i])] = true;
-        p.partial_bytes = std::max(p.partial_bytes, kai::mmq_partial_bytes(types[i], m, rows[i], k));
+        const bool h = !legacy && kai::mmq_uses_h(types[i], m, rows[i]);
+        (h ? p.has_h : p.has_plane)[kai::mmq_layout(types[i])] = true;
+        p.partial_bytes = std::max(p.partial_bytes, kai::mmq_partial_bytes(types[i], m, rows[i], k, h));
     }
     size_t off = kai::align256(size_t(m) * sizeof(float));
     for (int l = 0; l < 3; ++l) {
         p.plane[l] = off;
         if (p.has_plane[l])
             off += kai::align256(m <= kai::MMQS_MAX_ROWS ? kai::mmqs_image_bytes(l, k) : kai::mmq_plane_bytes(m, k));
+    }
+    for (int l = 0; l < 3; ++l) {
+        if (!p.has_h[l]) continue;
+        p.h_codes[l] = off;
+        off += kai::align256(kai::mmqh_codes_bytes(m, k));
+        p.h_mins[l] = off;
+        off += kai::align256(kai::mmqh_mins_bytes(l, m, k));
     }
     p.partial = off;
     off += kai::align256(p.partial_bytes);
@@ -92,23 +104,33 @@ MmqScratch mmq_scratch(const int *types, const int64_t *rows, int count, int64_t
 }
 
 // One batched call on a prepared scratch: one preparation writes every plane (up to 16
-// rows: small-M image) the group reads, then one int8 GEMM per matrix stores its column
-// slice.
+// rows: small-M image) and fp16 image the group reads, then one GEMM per matrix stores its
+// column slice.
 void run_mmq_group(const void *const *weights, const int *types, const int64_t *rows, int count, const void *x,
                    int x_dtype, int64_t stride_x, int64_t k, int64_t m, void *dst, bool dst_bf16, int64_t ld,
                    char *scratch, const MmqScratch &plan, hipStream_t s) {
     const size_t elem = dst_bf16 ? 2 : 4;
     float *inverse = reinterpret_cast<float *>(scratch + plan.inverse);
-    uint8_t *planes[3];
-    for (int l = 0; l < 3; ++l)
-        planes[l] = plan.has_plane[l] ? reinterpret_cast<uint8_t *>(scratch + plan.plane[l]) : nullptr;
-    kai::launch_prepare_mmq(x, x_dtype, m, k, stride_x,
-                            kai::MmqPlanes{planes[0], planes[1], planes[2], inverse, m <= kai::MMQS_MAX_ROWS}, s);
+    kai::MmqPlanes planes{nullptr, nullptr, nullptr, inverse, m <= kai::MMQS_MAX_ROWS};
+    uint8_t **pl[3] = {&planes.d4, &planes.ds4, &planes.d2s6};
+    for (int l = 0; l < 3; ++l) {
+        if (plan.has_plane[l]) *pl[l] = reinterpret_cast<uint8_t *>(scratch + plan.plane[l]);
+        if (plan.has_h[l])
+            planes.h[l] = kai::MmqhImage{reinterpret_cast<uint8_t *>(scratch + plan.h_codes[l]),
+                                         reinterpret_cast<uint8_t *>(scratch + plan.h_mins[l])};
+    }
+    kai::launch_prepare_mmq(x, x_dtype, m, k, stride_x, planes, s);
+    float *partial = reinterpret_cast<float *>(scratch + plan.partial);
     int64_t col = 0;
     for (int i = 0; i < count; ++i) {
-        kai::launch_mmq_planes(types[i], weights[i], rows[i], k, m, planes[kai::mmq_layout(types[i])], inverse,
-                               reinterpret_cast<float *>(scratch + plan.partial), plan.partial_bytes,
-                               static_cast<char *>(dst) + col * elem, dst_bf16, ld, s);
+        const int l = kai::mmq_layout(types[i]);
+        char *out = static_cast<char *>(dst) + col * elem;
+        if (kai::mmq_uses_h(types[i], m, rows[i]))
+            kai::launch_mmq_h(types[i], weights[i], rows[i], k, m, planes.h[l], inverse, partial, plan.partial_bytes,
+                              out, dst_bf16, ld, s);
+        else
+            kai::launch_mmq_planes(types[i], weights[i], rows[i], k, m, *pl[l], inverse, partial, plan.partial_bytes,
+                                   out, dst_bf16, ld, s);
         col += rows[i];
     }
 }
@@ -147,7 +169,7 @@ void legacy_check(int type, int64_t n, int64_t k, int64_t m, bool batched) {
 }
 
 size_t legacy_scratch(int type, int64_t n, int64_t k, int64_t m, bool batched) {
-    if (legacy_on_planes(type, batched)) return mmq_scratch(&type, &n, 1, k, m).total;
+    if (legacy_on_planes(type, batched)) return mmq_scratch(&type, &n, 1, k, m, true).total;
     return activation_bytes(m, k, 0);
 }
 
@@ -162,7 +184,7 @@ int legacy_mul_mat(bool batched, const void *weight, int type, int64_t row, cons
         const hipStream_t s = stream_of(stream);
         char *base = static_cast<char *>(scratch);
         if (legacy_on_planes(type, batched)) {
-            const MmqScratch plan = mmq_scratch(&type, &row, 1, k, vecs);
+            const MmqScratch plan = mmq_scratch(&type, &row, 1, k, vecs, true);
             const int layout = kai::mmq_layout(type);
             float *inverse = reinterpret_cast<float *>(base + plan.inverse);
             uint8_t *plane = reinterpret_cast<uint8_t *>(base + plan.plane[layout]);
@@ -437,4 +459,16 @@ extern "C" int kai_fused_mmq_run_noalloc(const void *const *weights, const int *
         }
         if (current != device) (void)hipSetDevice(current);
     });
+}
+
+// ---- measurement entry points (include/kai_peaks.h)
+extern "C" int kai_peak_mfma(int kind, int64_t iters, int blocks, int threads, float *out, uintptr_t stream) {
+    return entry([&] { kai::launch_peak_mfma(kind, iters, blocks, threads, out, stream_of(stream)); });
+}
+extern "C" int64_t kai_peak_mfma_ops(int kind) { return kai::peak_mfma_ops(kind); }
+extern "C" int kai_peak_lds(int64_t iters, int blocks, int threads, float *out, uintptr_t stream) {
+    return entry([&] { kai::launch_peak_lds(iters, blocks, threads, out, stream_of(stream)); });
+}
+extern "C" int kai_peak_copy(const void *src, void *dst, int64_t bytes, int blocks, uintptr_t stream) {
+    return entry([&] { kai::launch_peak_copy(src, dst, bytes, blocks, stream_of(stream)); });
 }

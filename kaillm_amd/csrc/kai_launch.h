@@ -148,7 +148,9 @@ void launch_mmq_decode(int type, const void *weight, int64_t n, int64_t k, int64
 void launch_mmq_planes(int type, const void *weight, int64_t n, int64_t k, int64_t m, const uint8_t *plane,
                        const float *inverse, float *partial, size_t partial_bytes, void *dst, bool dst_bf16,
                        int64_t stride_dst, hipStream_t stream, bool exact = false);
-size_t mmq_partial_bytes(int type, int64_t m, int64_t n, int64_t k);
+// Partial-sum scratch of an m-row product: the small-M GEMM's (m <= 16), or with h the fp16
+// GEMM's split-K sums.
+size_t mmq_partial_bytes(int type, int64_t m, int64_t n, int64_t k, bool h = false);
 
 // Batched path (kai_fused_mmq_run): activation planes of GGML's MMQ quantisation, one per
 // layout a matrix of the group reads (D4: Q8_0, Q6_K, IQ3_S; DS4: Q4_0, Q4_K; D2S6: Q2_K).
@@ -180,13 +182,56 @@ constexpr int mmqs_image_step(int layout) {
 __host__ __device__ inline int64_t mmqs_steps(int64_t k) { return (k + 255) / 256; }
 inline size_t mmqs_image_bytes(int layout, int64_t k) { return size_t(mmqs_steps(k)) * mmqs_image_step(layout); }
 
+// Above MMQS_MAX_ROWS rows the fp16 GEMM (kai_mmqh.cuh: Q4_K, Q4_0, Q8_0, IQ3_S and Q2_K) reads,
+// per layout, an fp16 image of the same quantisation, rows padded to mmqh_mpad(m) with zeros
+// and K to mmqh_kpad(k), laid out as the GEMM's MFMA operands:
+//   codes  fp16 [kpad / 16][mpad][16]: each code times its block's scale, d * q rounded to fp32
+//          then to fp16, with d the scale the reference's block dot takes (D4: fp32 d; DS4 and
+//          D2S6: the stored fp16 d);
+//   mins   the min-pass operands per superblock (none for D4): DS4 fp16 [ceil(k / 256)][mpad][32]
+//          = [S_0..7 | Xhi_0..7 | Xlo_0..7 | 0 x 8], S the stored half(d * sum q) of the 8
+//          blocks and X = half(d) * sum q the exact block sums as high and low fp16 parts
+//          (hi = half(X), lo = half(X - hi)); D2S6 [..][mpad][64] = [Shi | Slo | Xhi | Xlo] over
+//          the 16 groups of 16 values, S the stored half sums (d * sum q for the last 32 values of
+//          each 128).
+inline int64_t mmqh_mpad(int64_t m) { return (m + 31) / 32 * 32; }
+inline int64_t mmqh_kpad(int64_t k) { return (k + 255) / 256 * 256; }  // whole 256-value steps
+inline size_t mmqh_codes_bytes(int64_t m, int64_t k) { return size_t(mmqh_kpad(k)) * size_t(mmqh_mpad(m)) * 2; }
+inline size_t mmqh_mins_bytes(int layout, int64_t m, int64_t k) {
+    return layout == MMQ_D4 ? 0 : size_t((k + 255) / 256) * size_t(mmqh_mpad(m)) * (layout == MMQ_DS4 ? 64 : 128);
+}
+struct MmqhImage {
+    uint8_t *codes = nullptr, *mins = nullptr;
+};
+
 struct MmqPlanes {
     uint8_t *d4, *ds4, *d2s6;  // null when no matrix of the group reads that layout
     float *inverse;
     bool image;          // small-M images (m <= MMQS_MAX_ROWS) instead of planes
     bool legacy = false;  // the legacy ops' quantisation (launch_prepare_legacy's), D4 / DS4 only
+    MmqhImage h[3] = {};  // the fp16 GEMM's images per layout (null codes when not read)
 };
+// Whether kai_fused_mmq_run's m-row product of an n-row matrix with this type runs on the fp16
+// GEMM (reading the layout's fp16 image) rather than the int8 kernels (reading the plane). Up to
+// 96 rows a matrix of more than 16384 rows stays on the int8 tile kernel: its 272-and-more weight
+// tiles of 128 rows leave the fp16 GEMM's one workgroup per CU a partial second round (measured
+// at 80 rows on 34816 x 5120 Q4_K: 111 us int8, 144 us fp16; 5120-row matrices: 90 / 63 us).
+inline bool mmq_uses_h(int type, int64_t m, int64_t n) {
+    return m > MMQS_MAX_ROWS && (m > 96 || n <= 16384) &&
+           (type == Q4_K || type == Q4_0 || type == Q8_0 || type == IQ3_S || type == Q2_K);
+}
+void launch_mmq_h(int type, const void *weight, int64_t n, int64_t k, int64_t m, const MmqhImage &image,
+                  const float *inverse, float *partial, size_t partial_bytes, void *dst, bool dst_bf16,
+                  int64_t stride_dst, hipStream_t stream);
+
 void launch_prepare_mmq(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const MmqPlanes &planes,
                         hipStream_t stream);
+
+// Measurement kernels (kai_peaks.hip): the MFMA rate of one instruction kind, the LDS read
+// rate and a streaming copy; kinds are the KAI_PEAK_* codes of include/kai_peaks.h.
+void launch_peak_mfma(int kind, int64_t iters, int blocks, int threads, float *out, hipStream_t stream);
+int64_t peak_mfma_ops(int kind);
+void launch_peak_lds(int64_t iters, int blocks, int threads, float *out, hipStream_t stream);
+void launch_peak_copy(const void *src, void *dst, int64_t bytes, int blocks, hipStream_t stream);
 
 }  // namespace kai

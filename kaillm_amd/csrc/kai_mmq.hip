@@ -101,9 +101,13 @@ void launch_mmq_planes(int type, const void *weight, int64_t n, int64_t k, int64
     dispatch<true>(type, weight, n, k, m, plane, inverse, dst, dst_bf16, stride_dst, stream);
 }
 
+size_t mmqh_partial_bytes_of(int type, int64_t m, int64_t n, int64_t k);  // kai_mmqh.hip
+
 // The small-M GEMM's partial sums, whichever GEMM the launch picks: the scratch query takes no
-// device, and a matrix the persistent GEMM takes leaves them unused.
-size_t mmq_partial_bytes(int type, int64_t m, int64_t n, int64_t k) {
+// device, and a matrix the persistent GEMM takes leaves them unused. h: the fp16 GEMM's
+// split-K sums.
+size_t mmq_partial_bytes(int type, int64_t m, int64_t n, int64_t k, bool h) {
+    if (h) return mmqh_partial_bytes_of(type, m, n, k);
     switch (type) {
 #define KAI_T(T) case T: return mmqs_partial_bytes<T>(m, n, k);
         KAI_T(Q8_0) KAI_T(Q4_0) KAI_T(Q4_K) KAI_T(Q6_K) KAI_T(Q2_K) KAI_T(IQ3_S)

@@ -1,6 +1,7 @@
-// MMQ instantiations for IQ3_S (kernel templates in kai_mmq.cuh, kai_mmqs.cuh
-// and kai_mmqd.cuh).
+// MMQ instantiations for IQ3_S (kernel templates in kai_mmq.cuh, kai_mmqs.cuh,
+// kai_mmqd.cuh and kai_mmqh.cuh).
 #include "kai_mmqd.cuh"
+#include "kai_mmqh.cuh"
 
 namespace kai {
 template void launch_mmq_type<IQ3_S, false>(const void *, int64_t, int64_t, int64_t, const void *, const float *, void *,
@@ -13,4 +14,6 @@ template void launch_mmqd<IQ3_S>(const void *, int64_t, int64_t, int64_t, const 
                              bool, int64_t, hipStream_t);
 template void launch_mmqd_image<IQ3_S>(const void *, int64_t, int64_t, int64_t, const uint8_t *, const float *,
                                     void *, bool, int64_t, hipStream_t);
+template void launch_mmqh<IQ3_S>(const void *, int64_t, int64_t, int64_t, const MmqhArgs &, const float *, float *,
+                              size_t, void *, bool, int64_t, hipStream_t);
 }  // namespace kai

@@ -1,6 +1,7 @@
-// MMQ instantiations for Q8_0 (kernel templates in kai_mmq.cuh, kai_mmqs.cuh
-// and kai_mmqd.cuh).
+// MMQ instantiations for Q8_0 (kernel templates in kai_mmq.cuh, kai_mmqs.cuh,
+// kai_mmqd.cuh and kai_mmqh.cuh).
 #include "kai_mmqd.cuh"
+#include "kai_mmqh.cuh"
 
 namespace kai {
 template void launch_mmq_type<Q8_0, false>(const void *, int64_t, int64_t, int64_t, const void *, const float *, void *,
@@ -13,4 +14,6 @@ template void launch_mmqd<Q8_0>(const void *, int64_t, int64_t, int64_t, const b
                              bool, int64_t, hipStream_t);
 template void launch_mmqd_image<Q8_0>(const void *, int64_t, int64_t, int64_t, const uint8_t *, const float *,
                                     void *, bool, int64_t, hipStream_t);
+template void launch_mmqh<Q8_0>(const void *, int64_t, int64_t, int64_t, const MmqhArgs &, const float *, float *,
+                              size_t, void *, bool, int64_t, hipStream_t);
 }  // namespace kai

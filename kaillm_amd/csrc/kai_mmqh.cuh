@@ -1,0 +1,678 @@
+// Batched GEMM for more than 16 activation rows (spec-verify m = 17..80, prefill m = 512..2048)
+// on fp16 MFMA with the block scales folded into the operands: kai_fused_mmq_run's product for
+// Q4_K, Q4_0, Q8_0, IQ3_S and Q2_K.
+//
+// Arithmetic. GGML MMQ (the reference's batched path, current_ggml_direct.cu:1196-1265) sums,
+// per 32-value block (16 for Q2_K), the integer dot of the activation codes q with the weight
+// codes c times the activation scale dx and the weight scale dw, minus the min terms. Here both
+// scales are folded into fp16 operands, x' = half(dx q) (written by the preparation) and
+// w' = half(dw (c - c0)) with the codes centred by c0 (Q4_K 8, Q2_K 2; Q4_0 carries its own
+// -8, Q8_0 and IQ3_S are signed), and the MFMA accumulates sum_k w'_k x'_k across all blocks
+// in fp32 with no per-block step. Per superblock one more MFMA pass adds the centring back,
+// c0 dw X with X = dx sum q the block's exact activation sum (high and low fp16 parts), and the
+// min terms -half(dmin m) S against the stored fp16 sums S, as the reference forms them. The
+// departure from the reference's arithmetic is the two fp16 roundings of w' and x' (2^-11
+// relative each; centring keeps the offset c0 dw from amplifying the activation rounding):
+// about 4e-4 of a row's largest output, against the 1e-3 the tests allow.
+//
+// Layout: D[j][i] with A = weights (32 weight rows j) and B = activations (32 activation rows
+// i). v_mfma_f32_32x32x16_f16 operands: lane l holds row / column l % 32, k = 8 * (l / 32)
+// .. +8; result: column l % 32, rows 8 * (r / 4) + 4 * (l / 32) + r % 4 for r = 0..15.
+//
+// Workgroup: 2 * GN * GM waves. The first GN * GM compute: each owns WN x WM tiles of 32 x 32,
+// BN = 32 WN GN weight rows by BM = 32 WM GM activation rows, and only reads LDS and runs
+// MFMAs. The other GN * GM produce: they load the activation image and the weights' wire bytes
+// and convert the weights. Waves w and w + GN GM share a SIMD (waves are dealt to the 4 SIMDs in
+// turn), so each SIMD runs one of each and the producer's VALU work overlaps the MFMAs. (A
+// compute wave that also converted would read MFMA results on the VALU or wait on memory in
+// the middle of its MFMA stream; either stalls the stream.)
+//
+// K runs in stages of 64 values (4 groups of 16), 4 stages a step (256 values, one superblock).
+// LDS, static arrays:
+//   * 2 activation stages, the codes [group 4][BM rows][32 B];
+//   * 2 weight stages, the folded codes [4][BN][32 B];
+//   * 2 raw weight steps, each row's wire bytes of one step [BN][RS] (copied 16 bytes a lane,
+//     consecutive lanes along a row, so that a wave's loads touch few cache lines);
+//   * the current superblock's min-pass operands, WMIN [BN][64 B] and AMIN [BM][AB].
+// In the code blocks the two 16-byte halves of row r are exchanged when bit 2 of r differs from
+// bit 3 (mmqh_swz): 8 or 16 lanes reading consecutive rows then hit distinct banks.
+//
+// Stage s, between two s_barriers:
+//   producers: load stage s + 3's activation chunks (ring of 4 stages in registers) and write
+//     stage s + 1's; at a step's first stage, write step i + 1's wire bytes (loaded a step
+//     earlier) to raw LDS and load step i + 2's; convert stage s + 1's weights from raw LDS;
+//   compute: stage s's MFMAs from LDS stage s % 2, at a step's first stage also the min pass.
+// The barrier is a bare s_barrier after lgkmcnt(0) (a memory fence would wait for every load in
+// flight). Every global load is issued unconditionally, clamped to the split's last stage at its
+// end, so that the compiler's count of loads in flight stays exact and each wait is for the
+// loads of two stages (wire bytes: a step) before.
+// Rows past the activation image and past the matrix are clamped; their outputs are never
+// stored. Split-K (grid.y > 1): each split writes its fp32 sums to scratch and
+// mmqh_reduce_kernel adds them in split order.
+#pragma once
+
+#include <type_traits>
+
+#include "kai_mmq_formats.h"
+
+namespace kai {
+
+typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
+typedef float v16f_t __attribute__((ext_vector_type(16)));
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+// The activation image of one layout (layout and sizes in kai_launch.h).
+struct MmqhArgs {
+    const uint8_t *codes, *mins;
+    int mpad;
+};
+
+__device__ __forceinline__ uint32_t h2_bits(h2_t v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ h2_t bits_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
+__device__ __forceinline__ h2_t h2_splat(uint32_t half_bits) { return bits_h2((half_bits & 0xffffu) * 0x10001u); }
+
+// Four bytes b (each 0..255) -> two words of fp16 (b - bias) * scale: fp16 1024 + b is exact,
+// and so is the subtraction; the product rounds once (v_pk_mul_f16).
+__device__ __forceinline__ uint2 bytes_to_h4(uint32_t w, float bias, h2_t scale) {
+    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u);
+    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u);
+    const h2_t b = {static_cast<_Float16>(1024.0f + bias), static_cast<_Float16>(1024.0f + bias)};
+    return make_uint2(h2_bits((bits_h2(lo) - b) * scale), h2_bits((bits_h2(hi) - b) * scale));
+}
+// 16 bytes -> 16 folded fp16 values (two uint4)
+__device__ __forceinline__ void bytes16_to_h(uint4 w, float bias, h2_t scale, uint4 &o0, uint4 &o1) {
+    const uint2 a = bytes_to_h4(w.x, bias, scale), b = bytes_to_h4(w.y, bias, scale),
+                c = bytes_to_h4(w.z, bias, scale), d = bytes_to_h4(w.w, bias, scale);
+    o0 = make_uint4(a.x, a.y, b.x, b.y);
+    o1 = make_uint4(c.x, c.y, d.x, d.y);
+}
+// fp16 bits of half(a * n) for fp16 a and a small integer n (exact in fp32, one rounding)
+__device__ __forceinline__ uint32_t half_times(float a, uint32_t n) { return float_to_half_bits(a * static_cast<float>(n)); }
+__device__ __forceinline__ uint32_t pack2(uint32_t lo, uint32_t hi) { return (lo & 0xffffu) | (hi << 16); }
+
+// Weight side per format. SEG: wire bytes of a row per step (256 values); RS: the raw LDS row
+// stride (SEG rounded up to 16, chosen so that 16 lanes reading consecutive rows at one offset
+// hit distinct banks); convert: the 32 folded values of unit (stage j4 of the step, half h) of a
+// row from its raw bytes (blocks from `valid` on, past the row's end, take the scale 0); C0 and
+// mins: the min-pass weight factors of a row, the 32 bytes at 32 h of its WMIN row (C0 = 0: no
+// min pass).
+template <int TYPE> struct MmqhW;
+
+// Q4_0 (vecdotq.cuh:46-66; GGML MMQ's tile takes the codes minus 8): block b = 2 j4 + h of
+// the step, 18 bytes: fp16 d, 16 bytes of nibbles (values 0-15 low, 16-31 high).
+template <> struct MmqhW<Q4_0> {
+    static constexpr int SEG = 144, RS = 144, C0 = 0;
+    static __device__ void convert(const lds_u8 *seg, int j4, int h, int valid, const uint32_t *, uint4 (&o)[4]) {
+        const int b = 2 * j4 + h;
+        const lds_u8 *p = seg + 18 * b;
+        const h2_t d = h2_splat(b < valid ? load_unaligned<uint16_t>(p) : 0u);
+        const uint4 q = load_unaligned<uint4>(p + 2);
+        const uint4 lo = make_uint4(q.x & 0x0f0f0f0fu, q.y & 0x0f0f0f0fu, q.z & 0x0f0f0f0fu, q.w & 0x0f0f0f0fu);
+        const uint4 hi = make_uint4((q.x >> 4) & 0x0f0f0f0fu, (q.y >> 4) & 0x0f0f0f0fu, (q.z >> 4) & 0x0f0f0f0fu,
+                                    (q.w >> 4) & 0x0f0f0f0fu);
+        bytes16_to_h(lo, 8.0f, d, o[0], o[1]);
+        bytes16_to_h(hi, 8.0f, d, o[2], o[3]);
+    }
+};
+
+// Q8_0 (vecdotq.cuh:165-177): block b = 2 j4 + h, 34 bytes: fp16 d, 32 int8 codes.
+template <> struct MmqhW<Q8_0> {
+    static constexpr int SEG = 272, RS = 272, C0 = 0;
+    static __device__ void convert(const lds_u8 *seg, int j4, int h, int valid, const uint32_t *, uint4 (&o)[4]) {
+        const int b = 2 * j4 + h;
+        const lds_u8 *p = seg + 34 * b;
+        const h2_t d = h2_splat(b < valid ? load_unaligned<uint16_t>(p) : 0u);
+        const uint4 q0 = load_unaligned<uint4>(p + 2), q1 = load_unaligned<uint4>(p + 18);
+        const uint32_t f = 0x80808080u;  // int8 -> x + 128
+        bytes16_to_h(make_uint4(q0.x ^ f, q0.y ^ f, q0.z ^ f, q0.w ^ f), 128.0f, d, o[0], o[1]);
+        bytes16_to_h(make_uint4(q1.x ^ f, q1.y ^ f, q1.z ^ f, q1.w ^ f), 128.0f, d, o[2], o[3]);
+    }
+};
+
+// IQ3_S (vecdotq.cuh:1649-1672; quants.py:1097-1125): block b = 2 j4 + h; eight grid entries
+// qs[8b + i] | (qh[b] bit i) << 8 of four levels, sign bits from signs[4b..]; the code times
+// the block scale (1 + 2 sc) is exact in fp16 (|code| <= 465), then times the superblock's d
+// (the one rounding).
+template <> struct MmqhW<IQ3_S> {
+    static constexpr int SEG = 110, RS = 112, C0 = 0;
+    static __device__ void convert(const lds_u8 *seg, int j4, int h, int, const uint32_t *grid, uint4 (&o)[4]) {
+        const int b = 2 * j4 + h;
+        const h2_t d = h2_splat(load_unaligned<uint16_t>(seg));
+        const uint2 qs = load_unaligned<uint2>(seg + 2 + 8 * b);
+        const uint32_t qh = seg[66 + b], signs = load_unaligned<uint32_t>(seg + 74 + 4 * b);
+        const uint32_t sc = (seg[106 + b / 2] >> (4 * (b & 1))) & 15u;
+        const _Float16 f = static_cast<_Float16>(static_cast<float>(1 + 2 * static_cast<int>(sc)));
+        const h2_t scode = {f, f}, one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+        uint32_t words[16];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t byte = ((i < 4 ? qs.x : qs.y) >> (8 * (i % 4))) & 0xffu;
+            const uint32_t idx = byte | (((qh >> i) & 1u) << 8);
+            // signed levels as int8 bytes -> + 128 -> fp16 levels (exact) -> * (1 + 2 sc) -> * d
+            const uint32_t v = Unit<IQ3_S>::signed_levels(grid[idx], (signs >> (4 * i)) & 0x0fu) ^ 0x80808080u;
+            const uint2 hv = bytes_to_h4(v, 128.0f, scode);
+            words[2 * i] = h2_bits(bits_h2(hv.x) * d * one);
+            words[2 * i + 1] = h2_bits(bits_h2(hv.y) * d * one);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[c] = make_uint4(words[4 * c], words[4 * c + 1], words[4 * c + 2], words[4 * c + 3]);
+    }
+};
+
+// Q4_K (load_tiles_q4_K of GGML MMQ; quants.py:480-502 for the scale packing): block
+// b = 2 j4 + h of the superblock, codes nibble h of qs[32 j4 ..]; dw = half(d sc_b),
+// mw = half(dmin m_b). WMIN row: [-mw_0..7 | 8 dw_0..7 | 8 dw_0..7 | 0 x 8] against the
+// activation's [S_0..7 | Xhi_0..7 | Xlo_0..7 | 0 x 8].
+template <> struct MmqhW<Q4_K> {
+    static constexpr int SEG = 144, RS = 144, C0 = 8;
+    static __device__ uint32_t sc6(uint4 hdr, int b) {
+        return b < 4 ? bits(hdr.y, 8 * b, 6) : bits(hdr.w, 8 * (b - 4), 4) | (bits(hdr.y, 8 * (b - 4) + 6, 2) << 4);
+    }
+    static __device__ uint32_t m6(uint4 hdr, int b) {
+        return b < 4 ? bits(hdr.z, 8 * b, 6) : bits(hdr.w, 8 * (b - 4) + 4, 4) | (bits(hdr.z, 8 * (b - 4) + 6, 2) << 4);
+    }
+    static __device__ void convert(const lds_u8 *seg, int j4, int h, int, const uint32_t *, uint4 (&o)[4]) {
+        const uint4 hdr = load_unaligned<uint4>(seg);
+        const uint4 q0 = load_unaligned<uint4>(seg + 16 + 32 * j4), q1 = load_unaligned<uint4>(seg + 32 + 32 * j4);
+        const int b = 2 * j4 + h, sh = 4 * h;
+        const h2_t dw = h2_splat(half_times(half_bits_to_float(hdr.x & 0xffffu), sc6(hdr, b)));
+        const uint4 n0 = make_uint4((q0.x >> sh) & 0x0f0f0f0fu, (q0.y >> sh) & 0x0f0f0f0fu,
+                                    (q0.z >> sh) & 0x0f0f0f0fu, (q0.w >> sh) & 0x0f0f0f0fu);
+        const uint4 n1 = make_uint4((q1.x >> sh) & 0x0f0f0f0fu, (q1.y >> sh) & 0x0f0f0f0fu,
+                                    (q1.z >> sh) & 0x0f0f0f0fu, (q1.w >> sh) & 0x0f0f0f0fu);
+        bytes16_to_h(n0, 8.0f, dw, o[0], o[1]);
+        bytes16_to_h(n1, 8.0f, dw, o[2], o[3]);
+    }
+    // h = 0: [-mw_0..7 | 8 dw_0..7]; h = 1: [8 dw_0..7 | 0]
+    static __device__ void mins(const lds_u8 *seg, int h, uint4 &o0, uint4 &o1) {
+        const uint4 hdr = load_unaligned<uint4>(seg);
+        const float d = half_bits_to_float(hdr.x & 0xffffu), dmin = half_bits_to_float(hdr.x >> 16);
+        uint32_t f[8], g[8];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            g[b] = float_to_half_bits(8.0f * half_bits_to_float(half_times(d, sc6(hdr, b))));  // exact: a power of 2
+            f[b] = half_times(dmin, m6(hdr, b)) ^ 0x8000u;  // -half(dmin m): the sign bit
+        }
+        const uint4 fg = make_uint4(pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7]));
+        const uint4 gg = make_uint4(pack2(g[0], g[1]), pack2(g[2], g[3]), pack2(g[4], g[5]), pack2(g[6], g[7]));
+        o0 = h ? gg : fg;
+        o1 = h ? make_uint4(0, 0, 0, 0) : gg;
+    }
+};
+
+// Q2_K (load_tiles_q2_K of GGML MMQ; quants.py:407-429): 32-value block kb = 2 j4 + h, codes
+// (qs[32 (kb / 4) + v] >> 2 (kb % 4)) & 3; two 16-value groups g = 2 kb, 2 kb + 1 with
+// dw = half(d sc_g), mw = half(dmin m_g) (scales[g]: low nibble sc, high nibble m). Centred
+// codes c - 2 are -2..1, so the folded values are exact. WMIN row: [-mw_0..15 | 2 dw_0..15]
+// against the activation's [Shi | Slo] and [Xhi | Xlo].
+template <> struct MmqhW<Q2_K> {
+    static constexpr int SEG = 84, RS = 112, C0 = 2;
+    static __device__ void convert(const lds_u8 *seg, int j4, int h, int, const uint32_t *, uint4 (&o)[4]) {
+        const int kb = 2 * j4 + h, sh = 2 * (kb % 4);
+        const uint4 q0 = load_unaligned<uint4>(seg + 16 + 32 * (kb / 4)),
+                    q1 = load_unaligned<uint4>(seg + 32 + 32 * (kb / 4));
+        const uint32_t pair = load_unaligned<uint16_t>(seg + 2 * kb);  // scale bytes 2 kb, 2 kb + 1
+        const float d = half_bits_to_float(load_unaligned<uint16_t>(seg + 80));
+        const h2_t dw0 = h2_splat(half_times(d, pair & 15u)), dw1 = h2_splat(half_times(d, (pair >> 8) & 15u));
+        const uint32_t m3 = 0x03030303u;
+        bytes16_to_h(make_uint4((q0.x >> sh) & m3, (q0.y >> sh) & m3, (q0.z >> sh) & m3, (q0.w >> sh) & m3), 2.0f,
+                     dw0, o[0], o[1]);
+        bytes16_to_h(make_uint4((q1.x >> sh) & m3, (q1.y >> sh) & m3, (q1.z >> sh) & m3, (q1.w >> sh) & m3), 2.0f,
+                     dw1, o[2], o[3]);
+    }
+    // h = 0: -mw of groups 0..15; h = 1: 2 dw of groups 0..15
+    static __device__ void mins(const lds_u8 *seg, int h, uint4 &o0, uint4 &o1) {
+        const uint4 sc = load_unaligned<uint4>(seg);
+        const uint32_t dm = load_unaligned<uint32_t>(seg + 80);
+        const float d = half_bits_to_float(dm & 0xffffu), dmin = half_bits_to_float(dm >> 16);
+        const uint32_t w[4] = {sc.x, sc.y, sc.z, sc.w};
+        uint32_t f[16];
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            const uint32_t byte = (w[g / 4] >> (8 * (g % 4))) & 0xffu;
+            f[g] = h ? float_to_half_bits(2.0f * half_bits_to_float(half_times(d, byte & 15u)))
+                     : half_times(dmin, byte >> 4) ^ 0x8000u;
+        }
+        o0 = make_uint4(pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7]));
+        o1 = make_uint4(pack2(f[8], f[9]), pack2(f[10], f[11]), pack2(f[12], f[13]), pack2(f[14], f[15]));
+    }
+};
+
+template <int TYPE> constexpr bool mmqh_type() {
+    return TYPE == Q4_K || TYPE == Q4_0 || TYPE == Q8_0 || TYPE == IQ3_S || TYPE == Q2_K;
+}
+// Min-pass operand bytes per activation row and superblock (0: none).
+template <int TYPE> constexpr int mmqh_amin_bytes() { return TYPE == Q4_K ? 64 : TYPE == Q2_K ? 128 : 0; }
+
+template <int TYPE, int BN, int BM>
+struct MmqhLds {
+    static constexpr int ASTAGE = 128 * BM, WSTAGE = 128 * BN, RAW = BN * MmqhW<TYPE>::RS;
+    static constexpr int WMIN = MmqhW<TYPE>::C0 ? 64 * BN : 16;
+    static constexpr int AMIN = mmqh_amin_bytes<TYPE>() ? mmqh_amin_bytes<TYPE>() * BM : 16;
+    static constexpr int TOTAL = 2 * ASTAGE + 2 * WSTAGE + 2 * RAW + WMIN + AMIN + (TYPE == IQ3_S ? 2048 : 0);
+};
+
+// byte of 16-byte half h of row r within a group's [rows][32 B] block
+__host__ __device__ constexpr int mmqh_swz(int r, int h) { return 32 * r + 16 * (h ^ (((r >> 2) ^ (r >> 3)) & 1)); }
+
+// this wave's LDS writes are done, then every wave of the workgroup meets (no fence)
+__device__ __forceinline__ void mmqh_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int TYPE, int WN, int WM, int GN, int GM>
+__global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2, 2))) void mmqh_kernel(
+    const uint8_t *__restrict__ weight, int64_t row_bytes, int n, int k, MmqhArgs img, int m,
+    const float *__restrict__ inverse, void *__restrict__ dst, int64_t stride_dst, int dst_bf16,
+    float *__restrict__ partial, int tiles_n, int tiles_m, int split_stages) {
+    using W = MmqhW<TYPE>;
+    constexpr int CW = GN * GM, THREADS = 64 * CW, BN = 32 * WN * GN, BM = 32 * WM * GM;
+    constexpr int AB = mmqh_amin_bytes<TYPE>();
+    constexpr bool SHORT = block_elems(TYPE) == 32;  // K may end inside a step
+    using L = MmqhLds<TYPE, BN, BM>;
+    constexpr int UNITS = 2 * BN, UPT = UNITS / THREADS;  // weight units per producer thread and stage
+    static_assert(UNITS % THREADS == 0 && (8 * BM) % THREADS == 0, "whole units and copies per producer thread");
+    __shared__ __align__(16) uint8_t act_lds0[L::ASTAGE];
+    __shared__ __align__(16) uint8_t act_lds1[L::ASTAGE];
+    __shared__ __align__(16) uint8_t wt_lds0[L::WSTAGE];
+    __shared__ __align__(16) uint8_t wt_lds1[L::WSTAGE];
+    __shared__ __align__(16) uint8_t raw_lds0[L::RAW];
+    __shared__ __align__(16) uint8_t raw_lds1[L::RAW];
+    __shared__ __align__(16) uint8_t wmin_lds[L::WMIN];
+    __shared__ __align__(16) uint8_t amin_lds[L::AMIN];
+    __shared__ uint32_t grid_lds[TYPE == IQ3_S ? 512 : 1];
+    lds_u8 *const A0 = (lds_u8 *)act_lds0, *const A1 = (lds_u8 *)act_lds1;
+    lds_u8 *const W0 = (lds_u8 *)wt_lds0, *const W1 = (lds_u8 *)wt_lds1;
+    lds_u8 *const R0 = (lds_u8 *)raw_lds0, *const R1 = (lds_u8 *)raw_lds1;
+    lds_u8 *const wmin = (lds_u8 *)wmin_lds, *const amin = (lds_u8 *)amin_lds;
+
+    const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
+    // tile of this workgroup: each XCD (workgroups dealt round-robin over 8) gets a contiguous
+    // range of tiles, weight tiles fastest, so the workgroups running together on an XCD share
+    // an activation tile in its L2
+    const int tiles = tiles_n * tiles_m;
+    int t = blockIdx.x;
+    if (tiles % 8 == 0) t = (t % 8) * (tiles / 8) + t / 8;
+    const int n0 = (t % tiles_n) * BN, m0 = (t / tiles_n) * BM;
+    // K runs to the image's padding, whole steps of 256 values; split_stages is a multiple of 4,
+    // so every split is whole steps and s % 4 is the stage's place in its step
+    const int stages = (k + 255) / 256 * 4;
+    const int s0 = blockIdx.y * split_stages, s1 = min(stages, s0 + split_stages), last = s1 - 1;
+    if constexpr (TYPE == IQ3_S) {
+        for (int i = tid; i < 512; i += 2 * THREADS) grid_lds[i] = mmq_iq3s_grid[i];
+    }
+    using J0 = std::integral_constant<int, 0>;
+    using J1 = std::integral_constant<int, 1>;
+    using J2 = std::integral_constant<int, 2>;
+    using J3 = std::integral_constant<int, 3>;
+
+    if (wave >= CW) {
+        // ================= producer waves
+        const int ptid = tid - THREADS;
+        // wire bytes: copy c of a step is row c / CPR, 16 bytes at 16 (c % CPR) of the row's step
+        // (the last copy ends at the step's last byte, overlapping the one before when the step
+        // is not a multiple of 16 bytes, so that no copy reads past the row's step)
+        constexpr int CPR = (W::SEG + 15) / 16, RAWC = BN * CPR, RPT = (RAWC + THREADS - 1) / THREADS;
+        const uint8_t *raw_row[RPT];
+        int raw_at[RPT], raw_piece[RPT];
+#pragma unroll
+        for (int p = 0; p < RPT; ++p) {
+            const int c = min(ptid + p * THREADS, RAWC - 1), r = c / CPR;
+            raw_row[p] = weight + int64_t(min(n0 + r, n - 1)) * row_bytes;
+            raw_at[p] = r * W::RS;
+            raw_piece[p] = 16 * (c % CPR);
+        }
+        const int nblocks = k / QK8_1;
+        uint4 rawv[RPT];
+        int raw_off[RPT];
+        auto rload = [&](int step) __attribute__((always_inline)) {
+            // bytes of the row in this step (short formats: the last step may hold fewer blocks)
+            const int have = SHORT ? min(W::SEG, static_cast<int>(row_bytes - int64_t(step) * W::SEG)) : W::SEG;
+#pragma unroll
+            for (int p = 0; p < RPT; ++p) {
+                raw_off[p] = min(raw_piece[p], have - 16);
+                rawv[p] = load_unaligned<uint4>(raw_row[p] + int64_t(step) * W::SEG + raw_off[p]);
+            }
+        };
+        auto rstore = [&](lds_u8 *rb) __attribute__((always_inline)) {
+#pragma unroll
+            for (int p = 0; p < RPT; ++p)
+                if (RAWC % THREADS == 0 || ptid + p * THREADS < RAWC) store_unaligned(rb + raw_at[p] + raw_off[p], rawv[p]);
+        };
+        // weights: unit u = h * BN + j (32 values of row j: half h of a stage)
+        // first: s is a superblock's first stage (its min-pass factors go to WMIN)
+        auto wstore = [&](int s, lds_u8 *wb, auto first) __attribute__((always_inline)) {
+            const lds_u8 *rb = ((s >> 2) & 1) ? R1 : R0;
+            const int valid = SHORT ? nblocks - 8 * (s >> 2) : 8;  // blocks of the step in the row
+#pragma unroll
+            for (int p = 0; p < UPT; ++p) {
+                const int u = ptid + p * THREADS, j = u % BN, h = u / BN;
+                uint4 c[4];
+                W::convert(rb + j * W::RS, s & 3, h, valid, grid_lds, c);
+                store16(wb + (2 * h) * BN * 32 + mmqh_swz(j, 0), c[0]);
+                store16(wb + (2 * h) * BN * 32 + mmqh_swz(j, 1), c[1]);
+                store16(wb + (2 * h + 1) * BN * 32 + mmqh_swz(j, 0), c[2]);
+                store16(wb + (2 * h + 1) * BN * 32 + mmqh_swz(j, 1), c[3]);
+                if constexpr (W::C0 != 0) {
+                    if constexpr (decltype(first)::value) {
+                        uint4 o0, o1;
+                        W::mins(rb + j * W::RS, h, o0, o1);
+                        store16(wmin + j * 64 + 32 * h, o0);
+                        store16(wmin + j * 64 + 32 * h + 16, o1);
+                    }
+                }
+            }
+        };
+        // activation: per stage, the image's 16-byte chunks (4 groups x BM rows x 32 bytes; chunk
+        // w of a group holds row w / 2, half (w % 2) swizzled), loaded two stages ahead (ring of
+        // 4 in registers) and written to LDS a stage ahead; per superblock its min-pass operands
+        // (BM x AB bytes). Rows past the image read its last row.
+        const int rows_here = min(BM, img.mpad - m0);
+        constexpr int MIN_CH = AB * BM / 16;
+        constexpr int CODE_PW = 8 * BM / THREADS, MIN_PW = (MIN_CH + THREADS - 1) / THREADS;
+        int code_src[CODE_PW], min_src[MIN_PW > 0 ? MIN_PW : 1];
+#pragma unroll
+        for (int p = 0; p < CODE_PW; ++p) {
+            const int c = ptid + p * THREADS, g = c / (2 * BM), w = c % (2 * BM), r = w >> 1;
+            const int hsrc = (w & 1) ^ (((r >> 2) ^ (r >> 3)) & 1);
+            code_src[p] = g * img.mpad * 32 + 32 * min(r, rows_here - 1) + 16 * hsrc;
+        }
+#pragma unroll
+        for (int p = 0; p < MIN_PW; ++p) min_src[p] = 16 * min(ptid + p * THREADS, rows_here * AB / 16 - 1);
+        auto aload = [&](int s, uint4 (&v)[CODE_PW]) __attribute__((always_inline)) {
+            const uint8_t *cb = img.codes + (int64_t(4 * s) * img.mpad + m0) * 32;
+#pragma unroll
+            for (int p = 0; p < CODE_PW; ++p) v[p] = *reinterpret_cast<const uint4 *>(cb + code_src[p]);
+        };
+        auto astore = [&](const uint4 (&v)[CODE_PW], lds_u8 *ab) __attribute__((always_inline)) {
+#pragma unroll
+            for (int p = 0; p < CODE_PW; ++p) store16(ab + 16 * (ptid + p * THREADS), v[p]);
+        };
+        uint4 mv[MIN_PW > 0 ? MIN_PW : 1];
+        auto mload = [&](int s) __attribute__((always_inline)) {  // s: a superblock's first stage
+            const uint8_t *mb = img.mins + (int64_t(s / 4) * img.mpad + m0) * AB;
+#pragma unroll
+            for (int p = 0; p < MIN_PW; ++p) mv[p] = *reinterpret_cast<const uint4 *>(mb + min_src[p]);
+        };
+        auto mstore = [&]() __attribute__((always_inline)) {
+#pragma unroll
+            for (int p = 0; p < MIN_PW; ++p)
+                if (MIN_CH % THREADS == 0 || ptid + p * THREADS < MIN_CH) store16(amin + 16 * (ptid + p * THREADS), mv[p]);
+        };
+        uint4 v0[CODE_PW], v1[CODE_PW], v2[CODE_PW], v3[CODE_PW];
+        // stage J of a step i (s = 4 i + J): load stage s + 3 into ring entry (J + 3) % 4, write
+        // stage s + 1 from entry (J + 1) % 4; the min-pass operands of a superblock are loaded
+        // with its first stage (J = 1 loads stage s + 3 = 4 i + 4) and written with it (J = 3
+        // writes stage s + 1); at J = 0 the wire bytes of step i + 1 (loaded at step i - 1) go
+        // to raw LDS and those of step i + 2 are loaded
+        auto pstep = [&](int s, auto jtag, lds_u8 *anext, lds_u8 *wnext, uint4 (&vload)[CODE_PW],
+                         const uint4 (&vstore)[CODE_PW]) __attribute__((always_inline)) {
+            constexpr int J = decltype(jtag)::value;
+            const int sl = min(s + 3, last), sw = min(s + 1, last), step = s >> 2;
+            if constexpr (J == 0) {
+                rstore(((step + 1) & 1) ? R1 : R0);
+                rload(min(step + 2, last >> 2));
+            }
+            if constexpr (MIN_PW > 0 && J == 1) mload(sl / 4 * 4);
+            aload(sl, vload);
+            astore(vstore, anext);
+            if constexpr (MIN_PW > 0 && J == 3) mstore();
+            wstore(sw, wnext, std::integral_constant<bool, J == 3>{});
+            mmqh_barrier();
+        };
+        if constexpr (TYPE == IQ3_S) mmqh_barrier();  // the grid, before the first conversion
+        if (s0 < s1) {
+            // the loads in the loop's order (wire bytes, then the activation stages), so that the
+            // compiler's count of loads in flight at the loop's head agrees with the loop's own
+            rload(s0 >> 2);
+            rstore(((s0 >> 2) & 1) ? R1 : R0);
+            rload(min((s0 >> 2) + 1, last >> 2));
+            if constexpr (MIN_PW > 0) mload(s0);
+            aload(s0, v0);
+            aload(min(s0 + 1, last), v1);
+            aload(min(s0 + 2, last), v2);
+            if constexpr (MIN_PW > 0) mstore();
+            astore(v0, A0);
+            mmqh_barrier();  // the wire bytes of the first step
+            wstore(s0, W0, std::true_type{});
+            mmqh_barrier();
+            for (int s = s0; s < s1; s += 4) {
+                pstep(s, J0{}, A1, W1, v3, v1);
+                pstep(s + 1, J1{}, A0, W0, v0, v2);
+                pstep(s + 2, J2{}, A1, W1, v1, v3);
+                pstep(s + 3, J3{}, A0, W0, v2, v0);
+            }
+        }
+        return;
+    }
+
+    // ================= compute waves
+    const int wn = wave % GN, wm = wave / GN;
+    const int col = lane & 31, kh = lane >> 5;
+    v16f_t acc[WN][WM];
+#pragma unroll
+    for (int a = 0; a < WN; ++a)
+#pragma unroll
+        for (int b = 0; b < WM; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+
+    // Lane (col, kh) reads operand row col of each tile, k half kh. The stage's operands are read
+    // up front, group by group, so that the first group's products start while the rest arrive;
+    // within a group the tiles' MFMAs are independent.
+    const int wrow0 = wn * 32 * WN, arow0 = wm * 32 * WM;
+    const int a_off = mmqh_swz(wrow0 + col, kh), b_off = mmqh_swz(arow0 + col, kh);
+    auto compute = [&](const lds_u8 *ab, const lds_u8 *wb, auto first) __attribute__((always_inline)) {
+        v8h_t a[4][WN], b[4][WM];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+#pragma unroll
+            for (int tn = 0; tn < WN; ++tn) a[g][tn] = load_unaligned<v8h_t>(wb + g * BN * 32 + 32 * 32 * tn + a_off);
+#pragma unroll
+            for (int tm = 0; tm < WM; ++tm) b[g][tm] = load_unaligned<v8h_t>(ab + g * BM * 32 + 32 * 32 * tm + b_off);
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int tn = 0; tn < WN; ++tn)
+#pragma unroll
+                for (int tm = 0; tm < WM; ++tm)
+                    acc[tn][tm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[g][tn], b[g][tm], acc[tn][tm], 0, 0, 0);
+        if constexpr (W::C0 != 0) {
+          if constexpr (decltype(first)::value) {
+            // the superblock's min pass: 64 bytes of weight factors against AB bytes of activation
+            // sums per row, 32 bytes per MFMA (lane kh takes the 16 at 16 kh). Q4_K:
+            // (-mw | 8 dw) x (S | Xhi), (8 dw | 0) x (Xlo | 0); Q2_K: -mw x Shi, -mw x Slo,
+            // 2 dw x Xhi, 2 dw x Xlo
+            constexpr int PASSES = AB / 32;
+            v8h_t am[2][WN], bm[PASSES][WM];
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+#pragma unroll
+                for (int tn = 0; tn < WN; ++tn)
+                    am[q][tn] = load_unaligned<v8h_t>(wmin + (wrow0 + 32 * tn + col) * 64 + 32 * q + 16 * kh);
+#pragma unroll
+            for (int q = 0; q < PASSES; ++q)
+#pragma unroll
+                for (int tm = 0; tm < WM; ++tm)
+                    bm[q][tm] = load_unaligned<v8h_t>(amin + (arow0 + 32 * tm + col) * AB + 32 * q + 16 * kh);
+#pragma unroll
+            for (int q = 0; q < PASSES; ++q)
+#pragma unroll
+                for (int tn = 0; tn < WN; ++tn)
+#pragma unroll
+                    for (int tm = 0; tm < WM; ++tm)
+                        acc[tn][tm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[PASSES == 2 ? q : q / 2][tn],
+                                                                             bm[q][tm], acc[tn][tm], 0, 0, 0);
+          }
+        }
+        mmqh_barrier();
+    };
+    if constexpr (TYPE == IQ3_S) mmqh_barrier();
+    if (s0 < s1) {
+        mmqh_barrier();  // the producers' wire bytes of the first step
+        mmqh_barrier();  // and its first stage
+        for (int s = s0; s < s1; s += 4) {
+            compute(A0, W0, std::true_type{});
+            compute(A1, W1, std::false_type{});
+            compute(A0, W0, std::false_type{});
+            compute(A1, W1, std::false_type{});
+        }
+    }
+
+    // ---- epilogue: lane (col, kh) holds activation row i = col of each activation tile and
+    // weight rows 8 q + 4 kh + (0..3) of each weight tile; one branch per kind of output
+    auto store_all = [&](auto kind_tag) __attribute__((always_inline)) {
+        constexpr int KIND = decltype(kind_tag)::value;  // 0 partial sums, 1 f32, 2 bf16
+#pragma unroll
+        for (int tm = 0; tm < WM; ++tm) {
+            const int i = m0 + arow0 + 32 * tm + col;
+            if (i >= m) continue;
+            const float inv = KIND == 0 ? 1.0f : inverse[i];
+            float *rowf = KIND == 0 ? partial + (int64_t(blockIdx.y) * m + i) * n
+                                    : static_cast<float *>(dst) + int64_t(i) * stride_dst;
+            uint16_t *rowh = static_cast<uint16_t *>(dst) + int64_t(i) * stride_dst;
+#pragma unroll
+            for (int tn = 0; tn < WN; ++tn) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int j0 = n0 + wrow0 + 32 * tn + 8 * q + 4 * kh;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if (j0 + e < n) {
+                            const float v = acc[tn][tm][4 * q + e] * inv;
+                            if constexpr (KIND == 2) rowh[j0 + e] = float_to_bf16_bits(v);
+                            else rowf[j0 + e] = v;
+                        }
+                    }
+                }
+            }
+        }
+    };
+    if (partial) store_all(std::integral_constant<int, 0>{});
+    else if (dst_bf16) store_all(std::integral_constant<int, 2>{});
+    else store_all(std::integral_constant<int, 1>{});
+}
+
+// Split-K sums: out[i][j] = inverse[i] * sum over splits in order.
+__global__ __launch_bounds__(256) void mmqh_reduce_kernel(const float *__restrict__ partial, int splits, int m, int n,
+                                                          const float *__restrict__ inverse, void *__restrict__ dst,
+                                                          int64_t stride_dst, int dst_bf16);
+
+// Tile configurations: (WN, WM, GN, GM).
+struct MmqhConfig {
+    int wn, wm, gn, gm;
+    int bn() const { return 32 * wn * gn; }
+    int bm() const { return 32 * wm * gm; }
+};
+
+// Launch plan of an m-row product. It depends only on the type and shape (sized for the 256
+// CUs of an MI355X), so the scratch query and the launch agree on any device.
+struct MmqhPlan {
+    MmqhConfig cfg;
+    int tiles_n = 0, tiles_m = 0, splits = 1, split_stages = 0;
+};
+constexpr int MMQH_CUS = 256;
+template <int TYPE, int WN, int WM, int GN, int GM>
+constexpr bool mmqh_fits() {
+    return MmqhLds<TYPE, 32 * WN * GN, 32 * WM * GM>::TOTAL <= 160 * 1024;
+}
+// One workgroup per CU: its 8 waves fill the 4 SIMDs two each (amdgpu_waves_per_eu(2, 2)).
+template <int TYPE, int WN, int WM, int GN, int GM>
+constexpr int mmqh_per_cu() {
+    static_assert(GN * GM == 4, "one compute and one producer wave per SIMD");
+    static_assert(MmqhLds<TYPE, 32 * WN * GN, 32 * WM * GM>::TOTAL <= 160 * 1024, "LDS");
+    return 1;
+}
+// Each configuration's time for the product, in units of one CU's time for one 32 x 32 tile of
+// the whole K: rounds of resident workgroups times the workgroup's tiles per split, plus the
+// split-K sums (written and read once); the fastest wins.
+template <int TYPE, int WN, int WM, int GN, int GM>
+inline void mmqh_consider(MmqhPlan &best, double &best_t, int64_t n, int64_t k, int64_t m) {
+    constexpr int BN = 32 * WN * GN, BM = 32 * WM * GM, PER = mmqh_per_cu<TYPE, WN, WM, GN, GM>();
+    const int stages = static_cast<int>((k + 255) / 256 * 4), quantum = 4;  // whole steps
+    const int64_t tn = (n + BN - 1) / BN, tm = (m + BM - 1) / BM, slots = int64_t(MMQH_CUS) * PER;
+    const double tile_time = double(WN * GN * WM * GM) * PER;  // per workgroup, at PER per CU
+    for (int want = 1; want <= 8; ++want) {
+        const int chunk = ((stages + want - 1) / want + quantum - 1) / quantum * quantum;
+        const int splits = (stages + chunk - 1) / chunk;
+        if (splits != want || (splits > 1 && chunk < 16)) continue;
+        const int64_t wgs = tn * tm * splits, rounds = (wgs + slots - 1) / slots;
+        // the sums: 8 bytes per output and split at ~5 TB/s, against ~4 TOPS per CU for a tile
+        const double reduce = splits > 1 ? double(splits) * double(m) * double(n) / (320.0 * double(k)) : 0.0;
+        const double t = double(rounds) * tile_time / splits + reduce;
+        if (t < best_t) {
+            best_t = t;
+            best.cfg = {WN, WM, GN, GM};
+            best.tiles_n = static_cast<int>(tn);
+            best.tiles_m = static_cast<int>(tm);
+            best.splits = splits;
+            best.split_stages = chunk;
+        }
+    }
+}
+template <int TYPE>
+inline MmqhPlan mmqh_plan(int64_t n, int64_t k, int64_t m) {
+    MmqhPlan best;
+    double t = 1e300;
+    if (m <= 96) {
+        mmqh_consider<TYPE, 1, 3, 4, 1>(best, t, n, k, m);
+    } else {
+        if constexpr (mmqh_fits<TYPE, 2, 4, 2, 2>()) {
+            if (m >= 256) mmqh_consider<TYPE, 2, 4, 2, 2>(best, t, n, k, m);
+            else mmqh_consider<TYPE, 2, 2, 2, 2>(best, t, n, k, m);
+        } else {
+            mmqh_consider<TYPE, 2, 2, 2, 2>(best, t, n, k, m);
+        }
+    }
+    return best;
+}
+inline size_t mmqh_partial_bytes(const MmqhPlan &p, int64_t m, int64_t n) {
+    return p.splits > 1 ? size_t(p.splits) * size_t(m) * size_t(n) * sizeof(float) : 0;
+}
+
+template <int TYPE, int WN, int WM, int GN, int GM>
+void launch_mmqh_cfg(const void *weight, int64_t n, int64_t k, int64_t m, const MmqhArgs &img, const float *inverse,
+                     float *partial, const MmqhPlan &p, void *dst, bool dst_bf16, int64_t stride_dst,
+                     hipStream_t stream) {
+    constexpr int BN = 32 * WN * GN, BM = 32 * WM * GM;
+    static_assert(MmqhLds<TYPE, BN, BM>::TOTAL <= 160 * 1024, "mmqh LDS");  // static arrays
+    const int64_t row_bytes = (k / block_elems(TYPE)) * block_bytes(TYPE);
+    const dim3 grid(static_cast<unsigned>(p.tiles_n * p.tiles_m), static_cast<unsigned>(p.splits));
+    mmqh_kernel<TYPE, WN, WM, GN, GM><<<grid, 128 * GN * GM, 0, stream>>>(
+        static_cast<const uint8_t *>(weight), row_bytes, static_cast<int>(n), static_cast<int>(k), img,
+        static_cast<int>(m), inverse, dst, stride_dst, dst_bf16 ? 1 : 0, p.splits > 1 ? partial : nullptr, p.tiles_n,
+        p.tiles_m, p.split_stages);
+    if (p.splits > 1)
+        mmqh_reduce_kernel<<<static_cast<unsigned>((m * n + 1023) / 1024), 256, 0, stream>>>(
+            partial, p.splits, static_cast<int>(m), static_cast<int>(n), inverse, dst, stride_dst, dst_bf16 ? 1 : 0);
+}
+
+template <int TYPE>
+void launch_mmqh(const void *weight, int64_t n, int64_t k, int64_t m, const MmqhArgs &img, const float *inverse,
+                 float *partial, size_t partial_bytes, void *dst, bool dst_bf16, int64_t stride_dst,
+                 hipStream_t stream) {
+    static_assert(mmqh_type<TYPE>(), "fp16 GEMM format");
+    const MmqhPlan p = mmqh_plan<TYPE>(n, k, m);
+    if (mmqh_partial_bytes(p, m, n) > partial_bytes || (p.splits > 1 && !partial))
+        throw Error("Scratch too small for the fp16 GEMM's split-K sums");
+    if (n * ((k / block_elems(TYPE)) * block_bytes(TYPE)) >= (int64_t(1) << 40)) throw Error("Matrix too large");
+    // the short formats' wire-byte copies are 16 bytes, within the row's last step: one block at least
+    if (k % block_elems(TYPE) || (k / block_elems(TYPE)) * block_bytes(TYPE) < 16) throw Error("Invalid fp16 GEMM shape");
+    const MmqhConfig &c = p.cfg;
+#define KAI_H(WN, WM, GN, GM) \
+    if (c.wn == WN && c.wm == WM && c.gn == GN && c.gm == GM) \
+        return launch_mmqh_cfg<TYPE, WN, WM, GN, GM>(weight, n, k, m, img, inverse, partial, p, dst, dst_bf16, \
+                                                     stride_dst, stream);
+    KAI_H(2, 2, 2, 2) KAI_H(1, 3, 4, 1)
+    if constexpr (mmqh_fits<TYPE, 2, 4, 2, 2>()) {
+        KAI_H(2, 4, 2, 2)
+    }
+#undef KAI_H
+    throw Error("fp16 GEMM configuration");
+}
+
+}  // namespace kai

@@ -458,10 +458,26 @@ __device__ __forceinline__ void legacy_mmq_lane(const MmqPlanes &p, int ib, int 
     }
 }
 
+// One lane's 8 values of block ib in the fp16 GEMM's image (layout in kai_launch.h): the
+// dequantised activation d * q of each code, the product rounded to fp32 then to fp16; 16-value
+// group 2 ib + part / 2, half part % 2.
+__device__ __forceinline__ void mmqh_codes_lane(const MmqhImage &h, int mpad, int ib, int row, int part,
+                                                const int8_t (&q)[8], float d) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = half_of_product(d, q[2 * i]) | (half_of_product(d, q[2 * i + 1]) << 16);
+    const size_t at = ((static_cast<size_t>(2 * ib + (part >> 1)) * mpad + row) * 16 + 8 * (part & 1)) * 2;
+    *reinterpret_cast<uint4 *>(h.codes + at) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+// high and low fp16 parts of an fp32 value: hi = half(v), lo = half(v - hi)
+__device__ __forceinline__ uint32_t half_hi(float v) { return float_to_half_bits(v); }
+__device__ __forceinline__ uint32_t half_lo(float v) { return float_to_half_bits(v - half_bits_to_float(half_hi(v))); }
+
 // LEGACY: the legacy ops' quantisation (no row normalisation, inverse 1, legacy_mmq_lane).
 template <int DTYPE, bool LEGACY>
 __global__ __launch_bounds__(PREP_THREADS) void prepare_mmq_kernel(
-    const typename Src<DTYPE>::T *__restrict__ x, int64_t stride_x, int k, int m, int kpad_blocks, MmqPlanes p) {
+    const typename Src<DTYPE>::T *__restrict__ x, int64_t stride_x, int k, int m, int kpad_blocks, int hblocks, int mpad,
+    MmqPlanes p) {
     __shared__ float wave_max_lds[PREP_THREADS / WAVE];
     const int row = blockIdx.x;  // images: rows m..15 are written as zeros
     const int nblocks = k / QK8_1;
@@ -493,33 +509,68 @@ __global__ __launch_bounds__(PREP_THREADS) void prepare_mmq_kernel(
     const int sub = ib & 3;  // 32-value block within the 128-value block
     const size_t blk = (static_cast<size_t>(ib >> 2) * static_cast<size_t>(m) + static_cast<size_t>(row)) * MMQ_BLOCK_BYTES;
     const size_t codes = blk + 16 + 32 * sub + 8 * part;
-    if (p.d4 || p.ds4) {
+    const bool plane_row = row < m;  // rows past m exist only in the fp16 images (zeros)
+    // fp16 images: codes and scale records to K padded to 64, min operands to whole superblocks
+    const bool h_block = ib < hblocks, h_min = ib < 8 * ((k + 255) / 256);
+    if (p.d4 || p.ds4 || p.h[MMQ_D4].codes || p.h[MMQ_DS4].codes) {
         int8_t q[8];
         int s;
         const float d = mmq_group_codes<32>(v, q, s);
         const uint2 packed = pack_codes(q);
-        if (p.d4) {
+        const int total = quad_sum(s);
+        if (p.d4 && plane_row) {
             *reinterpret_cast<uint2 *>(p.d4 + codes) = packed;
             if (part == 0) *reinterpret_cast<float *>(p.d4 + blk + 4 * sub) = d;
         }
-        if (p.ds4) {
+        if (p.ds4 && plane_row) {
             *reinterpret_cast<uint2 *>(p.ds4 + codes) = packed;
-            const int total = quad_sum(s);
             if (part == 0)
                 *reinterpret_cast<uint32_t *>(p.ds4 + blk + 4 * sub) =
                     static_cast<uint32_t>(float_to_half_bits(d)) | (half_of_product(d, total) << 16);
         }
+        if (const MmqhImage &h = p.h[MMQ_DS4]; h.codes && h_min && part == 0) {
+            // [S_0..7 | Xhi_0..7 | Xlo_0..7 | 0 x 8]: the stored sum, and the exact sum half(d) * sum q
+            uint16_t *mn = reinterpret_cast<uint16_t *>(h.mins + (static_cast<size_t>(ib >> 3) * mpad + row) * 64);
+            const float x = half_bits_to_float(float_to_half_bits(d)) * static_cast<float>(total);
+            mn[ib & 7] = static_cast<uint16_t>(half_of_product(d, total));
+            mn[8 + (ib & 7)] = static_cast<uint16_t>(half_hi(x));
+            mn[16 + (ib & 7)] = static_cast<uint16_t>(half_lo(x));
+            mn[24 + (ib & 7)] = 0;
+        }
+        if (h_block) {
+            if (const MmqhImage &h = p.h[MMQ_D4]; h.codes) mmqh_codes_lane(h, mpad, ib, row, part, q, d);
+            if (const MmqhImage &h = p.h[MMQ_DS4]; h.codes)
+                mmqh_codes_lane(h, mpad, ib, row, part, q, half_bits_to_float(float_to_half_bits(d)));
+        }
     }
-    if (p.d2s6) {
+    if (p.d2s6 || p.h[MMQ_D2S6].codes) {
         int8_t q[8];
         int s;
         const float d = mmq_group_codes<64>(v, q, s);
-        *reinterpret_cast<uint2 *>(p.d2s6 + codes) = pack_codes(q);
         const int s16 = s + dpp_i32<DPP_QUAD_1032>(s);  // lanes {0,1} and {2,3}: 16 values each
         const int slot = 2 * sub + (part >> 1);
-        uint16_t *hdr = reinterpret_cast<uint16_t *>(p.d2s6 + blk);
-        if ((part & 1) == 0 && slot < 6) hdr[2 + slot] = static_cast<uint16_t>(half_of_product(d, s16));
-        if ((sub & 1) == 0 && part == 0) hdr[sub >> 1] = float_to_half_bits(d);
+        if (p.d2s6 && plane_row) {
+            *reinterpret_cast<uint2 *>(p.d2s6 + codes) = pack_codes(q);
+            uint16_t *hdr = reinterpret_cast<uint16_t *>(p.d2s6 + blk);
+            if ((part & 1) == 0 && slot < 6) hdr[2 + slot] = static_cast<uint16_t>(half_of_product(d, s16));
+            if ((sub & 1) == 0 && part == 0) hdr[sub >> 1] = float_to_half_bits(d);
+        }
+        if (const MmqhImage &h = p.h[MMQ_D2S6]; h.codes) {
+            const float dh = half_bits_to_float(float_to_half_bits(d));
+            if (h_block) mmqh_codes_lane(h, mpad, ib, row, part, q, dh);
+            if (h_min && (part & 1) == 0) {
+                // [Shi | Slo | Xhi | Xlo] per 16-value group: the stored half sums (d * sum q for the
+                // last 32 values of each 128), and the exact sums half(d) * sum q
+                const float sum = slot < 6 ? half_bits_to_float(half_of_product(d, s16)) : dh * static_cast<float>(s16);
+                const float x = dh * static_cast<float>(s16);
+                uint16_t *mn = reinterpret_cast<uint16_t *>(h.mins + (static_cast<size_t>(ib >> 3) * mpad + row) * 128);
+                const int g = 2 * (ib & 7) + (part >> 1);
+                mn[g] = static_cast<uint16_t>(half_hi(sum));
+                mn[16 + g] = static_cast<uint16_t>(half_lo(sum));
+                mn[32 + g] = static_cast<uint16_t>(half_hi(x));
+                mn[48 + g] = static_cast<uint16_t>(half_lo(x));
+            }
+        }
     }
 }
 
@@ -553,15 +604,18 @@ template <int DTYPE>
 static void launch_prepare_mmq_dtype(const void *x, int64_t m, int64_t k, int64_t stride_x, const MmqPlanes &p,
                                      hipStream_t stream) {
     const int kpad_blocks = static_cast<int>(mmq_blocks128(k) * 4);
-    const int64_t rows = p.image ? MMQS_MAX_ROWS : m;  // images: the zero rows too
+    const bool any_h = p.h[0].codes || p.h[1].codes || p.h[2].codes;
+    // images: the zero rows too (small-M images to 16 rows, fp16 images to mmqh_mpad(m))
+    const int64_t rows = p.image ? MMQS_MAX_ROWS : any_h ? mmqh_mpad(m) : m;
+    const int hblocks = static_cast<int>(mmqh_kpad(k) / QK8_1), mpad = static_cast<int>(mmqh_mpad(m));
     const dim3 grid(static_cast<unsigned>(rows), static_cast<unsigned>((kpad_blocks + PREP_BLOCKS - 1) / PREP_BLOCKS));
     const auto *src = static_cast<const typename Src<DTYPE>::T *>(x);
     if (p.legacy)
         prepare_mmq_kernel<DTYPE, true><<<grid, dim3(PREP_THREADS), 0, stream>>>(
-            src, stride_x, static_cast<int>(k), static_cast<int>(m), kpad_blocks, p);
+            src, stride_x, static_cast<int>(k), static_cast<int>(m), kpad_blocks, hblocks, mpad, p);
     else
         prepare_mmq_kernel<DTYPE, false><<<grid, dim3(PREP_THREADS), 0, stream>>>(
-            src, stride_x, static_cast<int>(k), static_cast<int>(m), kpad_blocks, p);
+            src, stride_x, static_cast<int>(k), static_cast<int>(m), kpad_blocks, hblocks, mpad, p);
 }
 
 void launch_prepare_mmq(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const MmqPlanes &planes,
@@ -570,6 +624,8 @@ void launch_prepare_mmq(const void *x, int x_dtype, int64_t m, int64_t k, int64_
         throw Error("Invalid batched activation shape");
     if (planes.image && m > MMQS_MAX_ROWS) throw Error("Small-M images hold at most 16 activation rows");
     if (planes.legacy && planes.d2s6) throw Error("The legacy quantisation has no D2S6 layout");
+    if ((planes.legacy || planes.image) && (planes.h[0].codes || planes.h[1].codes || planes.h[2].codes))
+        throw Error("The fp16 GEMM's images take the batched quantisation above 16 rows");
     switch (x_dtype) {
         case 0: launch_prepare_mmq_dtype<0>(x, m, k, stride_x, planes, stream); break;
         case 1: launch_prepare_mmq_dtype<1>(x, m, k, stride_x, planes, stream); break;

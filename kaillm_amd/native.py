@@ -66,6 +66,15 @@ def _load(path: str):
         getattr(lib, name).restype = c_int
     lib.kai_quantize_rows.argtypes = [c_int, ptr, i64, i64, ptr, c_int]
     lib.kai_quantize_rows.restype = c_int
+    # measurement entry points (include/kai_peaks.h)
+    lib.kai_peak_mfma.argtypes = [c_int, i64, c_int, c_int, ptr, u64]
+    lib.kai_peak_mfma.restype = c_int
+    lib.kai_peak_mfma_ops.argtypes = [c_int]
+    lib.kai_peak_mfma_ops.restype = i64
+    lib.kai_peak_lds.argtypes = [i64, c_int, c_int, ptr, u64]
+    lib.kai_peak_lds.restype = c_int
+    lib.kai_peak_copy.argtypes = [ptr, ptr, i64, c_int, u64]
+    lib.kai_peak_copy.restype = c_int
     return lib
 
 

@@ -123,22 +123,64 @@ def _image_bytes(layout, k):
     return (k + 255) // 256 * (4608 if layout == O.D4 else 5632)
 
 
+H_TYPES = (O.Q4_K, O.Q4_0, O.Q8_0, O.IQ3_S, O.Q2_K)  # the fp16 GEMM's formats (above 16 rows)
+
+
+def _uses_h(qtype, m, n):
+    """The batched route rule: the fp16 GEMM above 16 rows for its formats, except that up to
+    96 rows a matrix of more than 16384 rows stays on the int8 tile kernel."""
+    return qtype in H_TYPES and m > 16 and (m > 96 or n <= 16384)
+
+
+def test_mmq_workspace_follows_the_route_rule(kai):
+    """A 34816-row Q4_K matrix at 80 rows reads the int8 DS4 plane; at 5120 rows, or at 97
+    rows, the fp16 image."""
+    a256 = lambda b: (b + 255) // 256 * 256
+    types = (ctypes.c_int * 1)(O.Q4_K)
+    for n, m, image in ((34816, 80, False), (5120, 80, True), (34816, 97, True)):
+        rows = (ctypes.c_int64 * 1)(n)
+        got = kai.kai_fused_mmq_workspace(0, types, rows, 1, 5120, m, 1)
+        base = a256(4 * m) + (_h_image_bytes(O.DS4, m, 5120) if image else a256(_plane_bytes(m, 5120)))
+        assert base <= got, (n, m)
+        assert _uses_h(O.Q4_K, m, n) == image
+        # the remainder is the fp16 GEMM's split-K sums (at most 8 splits of m x n fp32); the int8
+        # tile kernel has none
+        assert (got - base) % 256 == 0 and got - base <= a256(8 * m * n * 4), (n, m, got - base)
+        if not image:
+            assert got == base, (n, m, got - base)
+
+
+def _h_image_bytes(layout, m, k):
+    """The fp16 GEMM's image of one layout: codes and min-pass sums, each 256-aligned."""
+    a256 = lambda b: (b + 255) // 256 * 256
+    mpad, kpad = (m + 31) // 32 * 32, (k + 255) // 256 * 256
+    codes = kpad * mpad * 2
+    mins = 0 if layout == O.D4 else (k + 255) // 256 * mpad * (64 if layout == O.DS4 else 128)
+    return a256(codes) + a256(mins)
+
+
 def test_mmq_workspace_is_inverse_then_one_plane_per_layout(kai):
-    """[inverse m f32][D4][DS4][D2S6], each 256-aligned, a region only for a layout the group
-    reads (Q8_0/Q6_K/IQ3_S: D4; Q4_0/Q4_K: DS4; Q2_K: D2S6): a plane, or up to 16 rows the
-    small-M image (per 256-value step 4608 bytes for D4, 5632 with the term arrays), followed
-    by the small-M GEMM's partial sums (16 x 16 fp32 per piece of a 16-row set, fewer pieces
-    per set than K steps)."""
+    """[inverse m f32][D4][DS4][D2S6], each 256-aligned, a region only for a layout that a
+    matrix on the int8 kernels reads (Q8_0/Q6_K/IQ3_S: D4; Q4_0/Q4_K: DS4; Q2_K: D2S6): a
+    plane, or up to 16 rows the small-M image (per 256-value step 4608 bytes for D4, 5632 with
+    the term arrays); above 16 rows the fp16 GEMM's image of each layout its formats read (Q6_K
+    keeps the int8 plane); then the partial sums: the small-M GEMM's (16 x 16 fp32 per piece
+    of a 16-row set, fewer pieces per set than K steps) or the fp16 GEMM's split-K sums (m x n
+    fp32 per split, at most 8 splits)."""
     a256 = lambda b: (b + 255) // 256 * 256
     for tl, m, k in (((12,), 16, 5120), ((12, 14), 80, 17408), ((10, 21, 2), 33, 1024), ((8,), 9, 1056),
-                     ((14,), 16, 17408), ((10, 21, 2), 12, 4096)):
+                     ((14,), 16, 17408), ((10, 21, 2), 12, 4096), ((14, 21), 40, 5120), ((2,), 600, 1056)):
         types = (ctypes.c_int * len(tl))(*tl)
         rows = (ctypes.c_int64 * len(tl))(*([64] * len(tl)))
-        layouts = {O.mmq_layout(t) for t in tl}
         got = kai.kai_fused_mmq_workspace(0, types, rows, len(tl), k, m, 1)
         if m > 16:
-            assert got == a256(4 * m) + len(layouts) * a256(_plane_bytes(m, k))
+            planes = {O.mmq_layout(t) for t in tl if not _uses_h(t, m, 64)}
+            images = {O.mmq_layout(t) for t in tl if _uses_h(t, m, 64)}
+            want = a256(4 * m) + len(planes) * a256(_plane_bytes(m, k)) + sum(_h_image_bytes(l, m, k) for l in images)
+            extra = got - want
+            assert extra >= 0 and extra % 256 == 0 and extra <= a256(8 * m * 64 * 4), (tl, m, k, extra)
         else:
+            layouts = {O.mmq_layout(t) for t in tl}
             want = a256(4 * m) + sum(a256(_image_bytes(l, k)) for l in layouts)
             assert want <= got <= want + a256((k + 255) // 256 * 4 * 1024)
 
@@ -204,10 +246,14 @@ def test_legacy_op_workspace_and_argument_rules(kai):
             assert kai.kai_ggml_a8_workspace(qtype, 64, k, m, 0) == O.activation_bytes(m, k)
         for qtype in (O.Q4_0, O.Q2_K):
             assert kai.kai_ggml_a8_workspace(qtype, 64, k, m, 1) == O.activation_bytes(m, k)
+    a256 = lambda b: (b + 255) // 256 * 256
     for qtype in (O.Q4_K, O.Q8_0, O.Q6_K):
         for m in (9, 16, 17, 80):
             arr = lambda t, v: (t * 1)(v)
-            want = kai.kai_fused_mmq_workspace(0, arr(ctypes.c_int, qtype), arr(ctypes.c_int64, 5120), 1, 4096, m, 0)
+            if m <= 16:  # the same small-M images and partial sums as the fused batched entry
+                want = kai.kai_fused_mmq_workspace(0, arr(ctypes.c_int, qtype), arr(ctypes.c_int64, 5120), 1, 4096, m, 0)
+            else:  # the int8 kernels' plane (the fused entry's fp16 GEMM takes no legacy activation)
+                want = a256(4 * m) + a256(_plane_bytes(m, 4096))
             assert kai.kai_ggml_a8_workspace(qtype, 5120, 4096, m, 1) == want > 0
         assert kai.kai_ggml_a8_workspace(qtype, 5120, 4096, 1, 1) > O.activation_bytes(1, 4096)
     assert kai.kai_ggml_a8_workspace(O.IQ3_S, 64, 256, 9, 1) == 0

@@ -216,15 +216,68 @@ def host_bits(x_dev):
 
 def plane_offsets(m, k, layouts):
     """Scratch offsets of kai_fused_mmq_run: [inverse][D4][DS4][D2S6]..., each a plane, or
-    for up to 16 rows the small-M image."""
+    for up to 16 rows the small-M image; above 16 rows (every format of these tests on the fp16
+    GEMM) each layout's fp16 image as (codes, mins) offsets."""
     a256 = lambda b: (b + 255) // 256 * 256
     off = a256(4 * m)
     out = {}
+    if m <= 16:
+        for l in (O.D4, O.DS4, O.D2S6):
+            if l in layouts:
+                out[l] = off
+                off += a256(image_bytes(l, k))
+        return out
     for l in (O.D4, O.DS4, O.D2S6):
         if l in layouts:
-            out[l] = off
-            off += a256(image_bytes(l, k) if m <= 16 else O.mmq_blocks128(k) * m * 144)
+            codes, mins = (a256(len(part)) for part in h_image_parts(None, l, m, k))
+            out[l] = (off, off + codes)
+            off += codes + mins
     return out
+
+
+def h_image_parts(plane, layout, m, k):
+    """The fp16 GEMM's activation image (codes, min-pass sums as bytes) that the preparation
+    writes above 16 rows, re-laid in numpy from the oracle's plane [K/128][m][144]: rows padded
+    to a multiple of 32 and K to 256; codes fp16 [K/16][mpad][16] = half(float32(d * q)) with d
+    the scale the block dot takes (D4: the fp32 d, DS4 / D2S6: the stored fp16 d); mins (none
+    for D4) per superblock, DS4 fp16 [..][mpad][32] = [S | Xhi | Xlo | 0] (S the 8 stored sums,
+    X = half(d) * sum(q) exact, hi = half(X), lo = half(X - hi)), D2S6 [..][mpad][64] =
+    [Shi | Slo | Xhi | Xlo] per 16-value group. plane None: zero bytes of each size."""
+    mpad, kpad, sbs = (m + 31) // 32 * 32, (k + 255) // 256 * 256, (k + 255) // 256
+    codes = np.zeros((kpad // 16, mpad, 16), np.float16)
+    mins = np.zeros((sbs, mpad, 0 if layout == O.D4 else 32 if layout == O.DS4 else 64), np.float16)
+    if plane is None:
+        return codes.view(np.uint8).reshape(-1), mins.view(np.uint8).reshape(-1)
+    f32, f16 = np.float32, np.float16
+    q, d, sums = O.split_plane(plane, layout)  # q [m, Kpad512], d per 32 (D2S6: 64), sums
+    g = 64 if layout == O.D2S6 else 32
+    dk = np.repeat(d[:, :kpad // g].astype(f32), g, axis=1)
+    if layout != O.D4:
+        dk = dk.astype(f16).astype(f32)
+    codes[:, :m, :] = (dk * q[:, :kpad].astype(f32)).astype(f16).reshape(m, kpad // 16, 16).transpose(1, 0, 2)
+
+    def parts(v):
+        hi = v.astype(f16)
+        return hi, (v - hi.astype(f32)).astype(f16)
+
+    if layout == O.DS4:
+        dh = d[:, :8 * sbs].astype(f32).astype(f16).astype(f32)
+        x = dh * q[:, :256 * sbs].astype(np.int64).reshape(m, 8 * sbs, 32).sum(axis=2).astype(f32)
+        xhi, xlo = parts(x)
+        mins[:, :m, 0:8] = sums[:, :8 * sbs].astype(f16).reshape(m, sbs, 8).transpose(1, 0, 2)
+        mins[:, :m, 8:16] = xhi.reshape(m, sbs, 8).transpose(1, 0, 2)
+        mins[:, :m, 16:24] = xlo.reshape(m, sbs, 8).transpose(1, 0, 2)
+    elif layout == O.D2S6:
+        s16 = sums[:, :16 * sbs].astype(f32).copy()  # NaN where the plane stores none
+        d64 = np.repeat(d[:, :4 * sbs].astype(f32), 4, axis=1)
+        dh = d64.astype(f16).astype(f32)
+        qs = q[:, :256 * sbs].astype(np.int64).reshape(m, 16 * sbs, 16).sum(axis=2).astype(f32)
+        s16 = np.where(np.isnan(s16), d64 * qs, s16).astype(f32)
+        for at, v in ((0, s16), (32, dh * qs)):
+            hi, lo = parts(v)
+            mins[:, :m, at:at + 16] = hi.reshape(m, sbs, 16).transpose(1, 0, 2)
+            mins[:, :m, at + 16:at + 32] = lo.reshape(m, sbs, 16).transpose(1, 0, 2)
+    return codes.view(np.uint8).reshape(-1), mins.view(np.uint8).reshape(-1)
 
 
 def image_bytes(layout, k):
@@ -275,8 +328,9 @@ def small_m_image(plane, layout, k):
 @pytest.mark.parametrize("m,k", [(9, 256), (12, 2080), (16, 4096), (17, 1056), (80, 5120), (130, 2080)])
 def test_mmq_planes_bit_exact(kai, dtype, m, k):
     """The batched path's activation (row scale + GGML MMQ quantisation into D4, DS4 and
-    D2S6 planes, K padded to 512; up to 16 rows the small-M images of those planes) read
-    back from the scratch equals the oracle's bytes."""
+    D2S6 planes, K padded to 512) read back from the scratch equals the oracle's bytes, in the
+    form the GEMMs read it: up to 16 rows the small-M images of the planes, above 16 rows the
+    fp16 GEMM's images (h_image_parts)."""
     print(f"mmq planes dtype={dtype} m={m} k={k}", flush=True)
     rng = np.random.default_rng(m + k)
     kq = k if k % 256 == 0 else None
@@ -297,8 +351,12 @@ def test_mmq_planes_bit_exact(kai, dtype, m, k):
     got = scratch.cpu().numpy()
     for layout in layouts:
         plane, inverse = O.prepare_mmq(xs, layout, code)
-        want = small_m_image(plane, layout, k) if m <= 16 else plane.reshape(-1)
-        assert np.array_equal(got[offs[layout]:offs[layout] + want.size], want), O.LAYOUT_NAMES[layout]
+        if m <= 16:
+            want = small_m_image(plane, layout, k)
+            assert np.array_equal(got[offs[layout]:offs[layout] + want.size], want), O.LAYOUT_NAMES[layout]
+        else:
+            for name, part, at in zip(("codes", "mins"), h_image_parts(plane, layout, m, k), offs[layout]):
+                assert np.array_equal(got[at:at + part.size], part), (O.LAYOUT_NAMES[layout], name)
         assert np.array_equal(got[:4 * m].view(np.float32), inverse)
     assert O.normwise_rel(out.cpu().numpy(), batched_ref(mats, xs, code)) <= TOL_F32
 
