@@ -41,6 +41,7 @@
 // both: D column l%16, rows 4*(l/16) + i.
 #pragma once
 
+#include <atomic>
 #include <type_traits>
 
 #include "kai_mmq_formats.h"
@@ -93,17 +94,17 @@ __device__ __forceinline__ float plane_terms(const uint4 q0, const uint4 q1, uin
     return d8;
 }
 
-template <int TYPE, int TM>
-constexpr int mmq_buf_bytes() {  // one K step of MT activation rows in LDS
-    return 16 * TM * (8 * 32 + 8 * 4 + MmqW<TYPE>::NTERM * 4);
+template <int TYPE, int TM, bool PAIR = false>
+constexpr int mmq_buf_bytes() {  // one K step of MT activation rows in LDS (PAIR: 8 rows)
+    return (PAIR ? 8 : 16 * TM) * (8 * 32 + 8 * 4 + MmqW<TYPE>::NTERM * 4);
 }
 
 // LDS of a workgroup: the double-buffered activation steps of its k-groups (reused for the
 // K-split sums after the loop), then each wave's weight transpose buffers (TN row tiles of 16
 // rows, MmqsStream).
-template <int TYPE, int TM, int TN, int KS>
+template <int TYPE, int TM, int TN, int KS, bool PAIR = false>
 constexpr size_t mmq_act_lds_bytes() {
-    const size_t act = size_t(2) * KS * mmq_buf_bytes<TYPE, TM>();
+    const size_t act = size_t(2) * KS * mmq_buf_bytes<TYPE, TM, PAIR>();
     const size_t red = KS > 1 ? size_t(KS - 1) * (4 / KS) * WAVE * TM * TN * 4 * sizeof(float) : 0;
     return ((act > red ? act : red) + 15) / 16 * 16;
 }
@@ -115,9 +116,9 @@ template <int TYPE> constexpr int mmq_tile_tbuf() { return 16 * MmqsStream<TYPE>
 // 34816 x 5120 +11 % (8 rows) to +22 % (80) and Q2_K +11 % at 512 rows, whose direct loads
 // are whole 16-byte pieces already.
 template <int TYPE> constexpr bool mmq_streamed() { return TYPE == Q6_K || TYPE == IQ3_S; }
-template <int TYPE, int TM, int TN, int KS>
+template <int TYPE, int TM, int TN, int KS, bool PAIR = false>
 constexpr size_t mmq_lds_bytes() {
-    return mmq_act_lds_bytes<TYPE, TM, TN, KS>() +
+    return mmq_act_lds_bytes<TYPE, TM, TN, KS, PAIR>() +
            (mmq_streamed<TYPE>() ? size_t(MMQ_THREADS / WAVE) * TN * mmq_tile_tbuf<TYPE>() : 0);
 }
 
@@ -164,6 +165,13 @@ __device__ __forceinline__ void paired_step(const typename MmqLoad<TYPE>::Raw (&
     // lane's A row: activation row col % 8 of block 2c + col / 8; its D rows
     // 4*oct .. +4: activation rows 4*(oct % 2) .. +4 of block 2c + oct / 2
     const int mr = col & 7, hi = col >> 3, ob = oct >> 1;
+    // split scales: the superblock scale (the same for every block of the step) multiplies the
+    // step's sums once, at the end
+    v4f_t part[TN];
+    if constexpr (MODE == MMQ_ISPLIT) {
+#pragma unroll
+        for (int t = 0; t < TN; ++t) part[t] = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         const uint64_t aq =
@@ -178,25 +186,34 @@ __device__ __forceinline__ void paired_step(const typename MmqLoad<TYPE>::Raw (&
                            c1 = W::template codes<false>(w[t], 2 * c + 1, oct, grid);
             const v4i_t bv = {static_cast<int>(c0), static_cast<int>(c0 >> 32), static_cast<int>(c1),
                               static_cast<int>(c1 >> 32)};
-            const float sa = ob ? W::template scale<false>(w[t], 2 * c + 1) : W::template scale<false>(w[t], 2 * c);
             if constexpr (MODE == MMQ_ISPLIT) {
+                // all 32 values, and the second 16 alone: sl * (all - second) + sh * second
                 const bool first = W::first_half(oct);
-                const v4i_t r1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, first ? bv : zero, zero, 0, 0, 0);
+                const v4i_t ra = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, zero, 0, 0, 0);
                 const v4i_t r2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, first ? zero : bv, zero, 0, 0, 0);
                 const int sl = ob ? W::iscale(w[t], 4 * c + 2) : W::iscale(w[t], 4 * c);
                 const int sh = ob ? W::iscale(w[t], 4 * c + 3) : W::iscale(w[t], 4 * c + 1);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int x = __mul24(sl, r1[i]) + __mul24(sh, r2[i]);
-                    acc[t][i] = fmaf(d8[i] * sa, static_cast<float>(x), acc[t][i]);
+                    const int x = __mul24(sl, ra[i]) + __mul24(sh - sl, r2[i]);
+                    part[t][i] = fmaf(d8[i], static_cast<float>(x), part[t][i]);
                 }
             } else {
+                const float sa = ob ? W::template scale<false>(w[t], 2 * c + 1) : W::template scale<false>(w[t], 2 * c);
                 const v4i_t r = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, zero, 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(d8[i] * sa, static_cast<float>(r[i]), acc[t][i]);
             }
         }
         if constexpr (PHASED) __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (MODE == MMQ_ISPLIT) {
+#pragma unroll
+        for (int t = 0; t < TN; ++t) {
+            const float sa = W::template scale<false>(w[t], 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(sa, part[t][i], acc[t][i]);
+        }
     }
     if constexpr (NT > 0) {  // the terms go to D rows 0-7 (activation rows 0-7), A rows 8-15 zero
         const float *ta = reinterpret_cast<const float *>(base + TA_OFF);
@@ -210,6 +227,42 @@ __device__ __forceinline__ void paired_step(const typename MmqLoad<TYPE>::Raw (&
     }
 }
 
+// K pieces across the workgroups of one launch (the paired tile on long rows of matrices
+// with too few row sets to fill the chip): each launch takes a slot of partial sums and an
+// arrival count per group of workgroups that share output elements. The host rotates the slot per launch, so launches in flight at once on other
+// streams take other slots; more than KAI_ZSLOTS such launches overlapping on one device race.
+// Every launch leaves its counts at zero. The sums are written through to memory and read
+// past the caches (system-scope stores and loads), so a count needs only the writer's own
+// wait for its stores before it, not an agent-scope release (whose L2 write-back per
+// workgroup costs more than the split gains).
+constexpr int KAI_ZSLOTS = 4, KAI_ZCAP = 1 << 19, KAI_ZSETS = 8192;
+static __device__ float kai_zpart[KAI_ZSLOTS][KAI_ZCAP];
+static __device__ unsigned kai_zcount[KAI_ZSLOTS][KAI_ZSETS];
+inline unsigned kai_next_zslot() {
+    static std::atomic<unsigned> next{0};
+    return next.fetch_add(1, std::memory_order_relaxed) % KAI_ZSLOTS;
+}
+__device__ __forceinline__ void zpart_store(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ float zpart_load(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+// The wave's stores are acknowledged (vmcnt counts stores on this architecture).
+__device__ __forceinline__ void zpart_stores_done() {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    __asm__ volatile("" ::: "memory");
+}
+// Arrival at a count: true for the last of `pieces` arrivals (which clears the count). Called
+// by one lane after zpart_stores_done; the caller orders its later loads of the sums after it.
+__device__ __forceinline__ bool zpart_arrive_last(unsigned *count, int pieces) {
+    const unsigned arrived = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = arrived == static_cast<unsigned>(pieces - 1);
+    if (last) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return last;
+}
+
 // PAIR: up to 8 rows of decode Q8_1 blocks (act: block_q8_1 [m][k/32], k % 256 == 0);
 // otherwise the batched path's plane of the type's layout (act: uint8 plane), any k that is
 // a whole number of blocks (a short last step reads zero activations).
@@ -218,14 +271,15 @@ __device__ __forceinline__ void paired_step(const typename MmqLoad<TYPE>::Raw (&
 template <int TYPE, int TM, int TN, int KS, int DEPTH, bool PAIR, bool EXACT = false>
 __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
     const uint8_t *__restrict__ weight, int64_t row_bytes, int n, int k, const void *__restrict__ act,
-    int m, const float *__restrict__ inverse, void *__restrict__ dst, int64_t stride_dst, int dst_bf16) {
+    int m, const float *__restrict__ inverse, void *__restrict__ dst, int64_t stride_dst, int dst_bf16,
+    int zsteps, int zslot) {
     using W = MmqLoad<TYPE>;
     static_assert(!PAIR || TM == 1, "paired blocks use one tile of 8 activation rows");
     static_assert(!(PAIR && EXACT), "the paired tile's arithmetic is exact already");
     constexpr bool BATCHED = !PAIR && !EXACT;  // GGML MMQ's weight arithmetic
     constexpr int MODE = W::template mode<BATCHED>();  // decode (paired) or batched arithmetic
     constexpr int MT = PAIR ? 8 : 16 * TM, RG = 4 / KS, NT = W::NTERM;
-    constexpr int BUF = mmq_buf_bytes<TYPE, TM>();
+    constexpr int BUF = mmq_buf_bytes<TYPE, TM, PAIR>();
     constexpr int D8_OFF = MT * 8 * 32, TA_OFF = D8_OFF + MT * 8 * 4;
     constexpr int PAIRS = KS * MT * 8;  // (k-group, row, block) activation blocks per iteration
     constexpr int PP = (PAIRS + MMQ_THREADS - 1) / MMQ_THREADS;
@@ -235,7 +289,10 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
     const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
     const int rg = wave % RG, kg = wave / RG;
     const int col = lane % 16, oct = lane / 16;
-    const int nb = k / QK8_1, steps = (k + MMQ_STEP - 1) / MMQ_STEP;
+    // PAIR with zsteps > 0: this workgroup's K piece, steps [z * zsteps, (z + 1) * zsteps)
+    const int nb = k / QK8_1, all_steps = (k + MMQ_STEP - 1) / MMQ_STEP;
+    const int sbase = PAIR && zsteps > 0 ? static_cast<int>(blockIdx.z) * zsteps : 0;
+    const int steps = PAIR && zsteps > 0 ? min(all_steps - sbase, zsteps) : all_steps;
     const int iters = (steps + KS - 1) / KS;
     const int m0 = blockIdx.y * MT;
     const int nrow0 = blockIdx.x * (16 * TN * RG) + rg * 16 * TN;
@@ -257,7 +314,7 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
             if (idx < PAIRS && s < steps && row < m) {
                 if constexpr (PAIR) {
                     const uint8_t *src = reinterpret_cast<const uint8_t *>(
-                        static_cast<const block_q8_1 *>(act) + int64_t(row) * nb + 8 * s + b);
+                        static_cast<const block_q8_1 *>(act) + int64_t(row) * nb + 8 * (sbase + s) + b);
                     ads[p] = load_unaligned<uint32_t>(src);
                     aq0[p] = load_unaligned<uint4>(src + 4);
                     aq1[p] = load_unaligned<uint4>(src + 20);
@@ -320,7 +377,7 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
         uoff[i] = real ? r * S::SBP + 16 * c : 16 * S::SBP;  // a spare unit past the 16 rows
     }
     const uint32_t tail = static_cast<uint32_t>(int64_t(n) * row_bytes - 16);
-    lds_u8 *tbuf = (lds_u8 *)kai_mmq_lds + mmq_act_lds_bytes<TYPE, TM, TN, KS>() + wave * TN * mmq_tile_tbuf<TYPE>();
+    lds_u8 *tbuf = (lds_u8 *)kai_mmq_lds + mmq_act_lds_bytes<TYPE, TM, TN, KS, PAIR>() + wave * TN * mmq_tile_tbuf<TYPE>();
     struct Streamed {
         uint4 v[TN][S::UPL];
         uint32_t back[TN];  // 4 bits per unit: the bytes its load start was moved back
@@ -332,7 +389,7 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
     Slot wr[DEPTH];
     auto wload = [&](Slot &sl, int it) {
         if constexpr (STREAM) {
-            const uint32_t step = static_cast<uint32_t>(min(it * KS + kg, steps - 1)) * S::SB;
+            const uint32_t step = static_cast<uint32_t>(sbase + min(it * KS + kg, steps - 1)) * S::SB;
 #pragma unroll
             for (int t = 0; t < TN; ++t) {
                 const uint32_t base = static_cast<uint32_t>(nrow0 + 16 * t) * static_cast<uint32_t>(row_bytes) + step;
@@ -345,7 +402,7 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
                 }
             }
         } else if constexpr (PAIR) {
-            const int s = min(it * KS + kg, steps - 1);  // past the end: the last step again
+            const int s = sbase + min(it * KS + kg, steps - 1);  // past the end: the last step again
 #pragma unroll
             for (int t = 0; t < TN; ++t) W::load(sl.raw[t], wrow[t] + int64_t(s) * W::SB, oct, 8);
         } else {
@@ -532,6 +589,36 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[0][t][i] += __shfl_xor(acc[0][t][i], 32);
         if (oct >= 2) return;
+        if (zsteps > 0 && gridDim.z > 1) {
+            // K pieces: each wave writes its piece's sums to the launch's slot; the wave whose
+            // arrival is the last for its 16*TN weight rows adds the pieces in K order (the
+            // same sums whatever the arrival order) and stores them.
+            const int Z = static_cast<int>(gridDim.z), z = static_cast<int>(blockIdx.z);
+            float *part = kai_zpart[zslot];
+#pragma unroll
+            for (int t = 0; t < TN; ++t) {
+                const int c = nrow0 + 16 * t + col;
+                if (c < n)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) zpart_store(&part[(size_t(z) * n + c) * 8 + 4 * oct + i], acc[0][t][i]);
+            }
+            zpart_stores_done();
+            int last = 0;
+            if (lane == 0) last = zpart_arrive_last(&kai_zcount[zslot][blockIdx.x * RG + rg], Z) ? 1 : 0;
+            if (!__shfl(last, 0)) return;
+            __asm__ volatile("" ::: "memory");  // no load of the sums above the count
+#pragma unroll
+            for (int t = 0; t < TN; ++t) {
+                const int c = min(nrow0 + 16 * t + col, n - 1);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float v = 0.0f;
+                    for (int zz = 0; zz < Z; ++zz)
+                        v += zz == z ? acc[0][t][i] : zpart_load(&part[(size_t(zz) * n + c) * 8 + 4 * oct + i]);
+                    acc[0][t][i] = v;
+                }
+            }
+        }
     }
 
     // ---- epilogue: x inverse[m], F32 or BF16, strided store
@@ -557,24 +644,50 @@ __global__ __launch_bounds__(MMQ_THREADS) void mmq_kernel(
 
 template <int TYPE, int TM, int TN, int KS, bool PAIR = false, bool EXACT = false>
 static void launch_mmq_tile(const void *weight, int64_t n, int64_t k, const void *act, int64_t m,
-                            const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream) {
+                            const float *inverse, void *dst, bool dst_bf16, int64_t stride_dst, hipStream_t stream,
+                            int pieces = 1) {
     constexpr int MT = PAIR ? 8 : 16 * TM, ROWS = 16 * TN * (4 / KS);
     const int64_t row_bytes = (k / block_elems(TYPE)) * block_bytes(TYPE);
     if (n * row_bytes >= (int64_t(1) << 32)) throw Error("MMQ takes matrices below 4 GiB");
-    const size_t lds = mmq_lds_bytes<TYPE, TM, TN, KS>();
+    const size_t lds = mmq_lds_bytes<TYPE, TM, TN, KS, PAIR>();
     // weight steps in flight: one. Measured on MI355X with one / two / three steps: the
     // paired tile (whose loop has no branch, so its waits count the ring exactly) on Q6_K
     // 5120x17408 at 8 rows 37.5 / 41.1 / 43.6 us, Q4_K 7168x5120 12.0 / 14.1 / 14.8 us; the
     // tiled kernel at 32-80 rows one against two steps, Q4_0 -5..-13 %, Q6_K and Q2_K
-    // unchanged.
+    // unchanged. Again with K pieces, one against two steps at 8 rows (whole calls): Q6_K
+    // 5120x17408 30.1 / 40.8 us, 5120x6144 17.6 / 19.2 us, Q4_K 7168x5120 13.7 / 15.7 us.
     constexpr int DEPTH = 1;
     auto kernel = mmq_kernel<TYPE, TM, TN, KS, DEPTH, PAIR, EXACT>;
     static DeviceFlags lds_raised;
     raise_dynamic_lds(reinterpret_cast<const void *>(kernel), lds, lds_raised, "Cannot raise the MMQ dynamic LDS limit");
-    const dim3 grid(static_cast<unsigned>((n + ROWS - 1) / ROWS), static_cast<unsigned>((m + MT - 1) / MT));
+    // K pieces (paired tile only): as many as keep the whole grid resident at once (a second
+    // round of workgroups would double the time), at most `pieces`; whole turns of the KS
+    // k-groups per piece, no empty piece.
+    const int steps = static_cast<int>((k + MMQ_STEP - 1) / MMQ_STEP);
+    int zsteps = 0, z = 1, slot = 0;
+    if (PAIR && pieces > 1 && steps > 1) {
+        static const int per_cu = [&] {
+            int blocks = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, reinterpret_cast<const void *>(kernel),
+                                                             MMQ_THREADS, lds) != hipSuccess)
+                throw Error("Cannot query the MMQ occupancy");
+            return blocks;
+        }();
+        const int64_t wgs = (n + ROWS - 1) / ROWS;
+        pieces = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(pieces, int64_t(per_cu) * device_cu_count() / wgs)));
+        const int turns = (steps + KS - 1) / KS;  // a piece is whole turns of the KS k-groups
+        zsteps = (turns + pieces - 1) / pieces * KS;
+        z = (steps + zsteps - 1) / zsteps;
+        if (z < 2) zsteps = 0, z = 1;
+        const int64_t sets = (n + ROWS - 1) / ROWS * (4 / KS);
+        if (z * n * 8 > KAI_ZCAP || sets > KAI_ZSETS) zsteps = 0, z = 1;
+        else if (z > 1) slot = static_cast<int>(kai_next_zslot());
+    }
+    const dim3 grid(static_cast<unsigned>((n + ROWS - 1) / ROWS), static_cast<unsigned>((m + MT - 1) / MT),
+                    static_cast<unsigned>(z));
     kernel<<<grid, MMQ_THREADS, lds, stream>>>(static_cast<const uint8_t *>(weight), row_bytes, static_cast<int>(n),
                                                static_cast<int>(k), act, static_cast<int>(m), inverse, dst, stride_dst,
-                                               dst_bf16 ? 1 : 0);
+                                               dst_bf16 ? 1 : 0, zsteps, slot);
 }
 
 // Tile choice. Activation tile MT = 16*TM rows: all rows up to 64 (weights streamed
@@ -616,11 +729,18 @@ void launch_mmq_type(const void *weight, int64_t n, int64_t k, int64_t m, const 
     }
     const int key = tm * 100 + tn * 10 + ks;
     if constexpr (!PLANES) {  // one tile of 8 activation rows, two blocks per MFMA
+        // Too few row sets to fill the chip, and long rows: K pieces across workgroups, at
+        // most 8 (each piece's sums cost a round trip to memory and back, which K of fewer
+        // than 32 steps does not repay). Measured on MI355X at 8 rows: Q6_K 5120 x 17408
+        // (68 steps) 36.2 -> 30.2 us whole calls, 5120 x 6144 (24 steps) 17.7 -> 17.3 us,
+        // Q4_K 7168 x 5120 (20 steps) 13.8 -> 16.1 us.
+        const int pieces = found || k < 32 * MMQ_STEP ? 1 : 8;
         switch (key) {
 #define KAI_P(TN, KS) \
     case 100 + TN * 10 + KS: \
         if constexpr (TN == 1 || wide) \
-            launch_mmq_tile<TYPE, 1, TN, KS, true>(weight, n, k, act, m, inverse, dst, dst_bf16, stride_dst, stream); \
+            launch_mmq_tile<TYPE, 1, TN, KS, true>(weight, n, k, act, m, inverse, dst, dst_bf16, stride_dst, stream, \
+                                                   pieces); \
         return;
             KAI_P(2, 1) KAI_P(1, 1) KAI_P(2, 2) KAI_P(1, 2) KAI_P(1, 4)
 #undef KAI_P

@@ -162,14 +162,17 @@ template <> struct MmqW<Q6_K> {
         r.sc = load_unaligned<uint4>(p + 192);
         r.d = load_unaligned<uint16_t>(p + 208);
     }
+    // code - 32 = (high 2 bits - 2) * 16 + low nibble: the high bits select the int8 high
+    // nibble (0xE0, 0xF0, 0x00, 0x10) from a byte table (v_perm_b32, selectors 0-3 pick the
+    // second operand's bytes), the low nibble is OR-ed in.
+    static __device__ uint32_t codes4(uint32_t ql, uint32_t qh, int nshift, int hshift) {
+        const uint32_t hi = __builtin_amdgcn_perm(0u, 0x1000f0e0u, (qh >> hshift) & 0x03030303u);
+        return ((ql >> nshift) & 0x0f0f0f0fu) | hi;
+    }
     template <bool MMA> static __device__ uint64_t codes(const Raw &r, int b, int, const uint32_t *) {
         const int h = b / 4, s = b % 4;
-        const uint64_t ql = u64(r.ql[2 * h + (s & 1)]), qh = u64(r.qh[h]);
-        const uint64_t c = ((ql >> (4 * (s >> 1))) & 0x0f0f0f0f0f0f0f0full) | (((qh >> (2 * s)) & 0x0303030303030303ull) << 4);
-        // c - 32 per byte: flip bit 5 (6-bit two's complement), then sign-extend bit 5
-        const uint64_t t = c ^ 0x2020202020202020ull;
-        const uint64_t sign = t & 0x2020202020202020ull;
-        return t | (sign << 1) | (sign << 2);
+        const uint2 ql = r.ql[2 * h + (s & 1)], qh = r.qh[h];
+        return u64(make_uint2(codes4(ql.x, qh.x, 4 * (s >> 1), 2 * s), codes4(ql.y, qh.y, 4 * (s >> 1), 2 * s)));
     }
     static __device__ int iscale(const Raw &r, int g) {  // int8 scale of 16-value group g
         const uint32_t w = g < 4 ? r.sc.x : g < 8 ? r.sc.y : g < 12 ? r.sc.z : r.sc.w;

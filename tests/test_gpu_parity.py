@@ -464,6 +464,37 @@ def test_tiled_paired_decode_full_shapes(kai, qtype, m, n, k):
     assert np.isnan(out[:, n:]).all()
 
 
+# The tiled paired kernel on fewer workgroups than about 2 per CU, with K of 32 steps or
+# more, splits K across workgroups (pieces of whole K turns); the last piece to arrive adds
+# all pieces in K order, so repeated calls agree bit for bit, and each call leaves its
+# arrival counts at zero for the next. 321 row sets (the last ragged), 320, 448.
+PIECES = [(O.Q6_K, 8, 5128, 17408), (O.IQ3_S, 6, 5120, 17408), (O.Q4_K, 7, 7168, 8192), (O.Q6_K, 5, 5120, 12288)]
+
+
+@pytest.mark.parametrize("qtype,m,n,k", PIECES, ids=lambda v: str(v))
+def test_tiled_paired_k_pieces(kai, qtype, m, n, k):
+    print(f"tiled paired K pieces {O.NAMES[qtype]} m={m} n={n} k={k}", flush=True)
+    rng = np.random.default_rng(7 * n + k + m)
+    w = O.random_blocks(qtype, n, k, rng)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    act = gpu_prepare(kai, to_dev(x))
+    w_dev = to_dev(w)
+    out = gpu_mmvq(kai, qtype, w_dev, n, k, act, m)
+    # a smaller product in between (fewer rows and columns, same slots)
+    small_n, small_k = 2048, 2560
+    w2 = O.random_blocks(qtype, small_n, small_k, rng)
+    x2 = rng.standard_normal((5, small_k)).astype(np.float16)
+    act2 = gpu_prepare(kai, to_dev(x2))
+    out2 = gpu_mmvq(kai, qtype, to_dev(w2), small_n, small_k, act2, 5)
+    again = [gpu_mmvq(kai, qtype, w_dev, n, k, act, m) for _ in range(5)]
+    for a in again:
+        assert torch.equal(out, a), "K pieces are added in a fixed order"
+    ref = O.mul_mat(qtype, w, k, O.prepare(x), m, threads=16)
+    assert O.normwise_rel(out.cpu().numpy(), ref) <= TOL_F32
+    ref2 = O.mul_mat(qtype, w2, small_k, O.prepare(x2), 5)
+    assert O.normwise_rel(out2.cpu().numpy(), ref2) <= TOL_F32
+
+
 @pytest.mark.parametrize("qtype", [O.Q4_K, O.Q6_K, O.IQ3_S])
 def test_mmq_prefill_shape(kai, qtype):
     """A prefill-sized call (m = 512) on a full-width weight, bf16 activations."""
