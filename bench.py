@@ -12,9 +12,12 @@ Every timing is a replay of a captured HIP graph, HIP events on the replay strea
 rotating weight copies totalling >= 600 MB so the 256 MB Infinity Cache never holds the
 working set.
 
-* ``roofline``: the Q4_K gate/up decode kernel at batch 1, 2 and 8 (the GEMV, or the paired
-  int8 tile above the GEMV's row limit), kernel only: the activation is prepared once
-  outside the graph; 100 270 080 weight bytes per launch over the mean launch time.
+* ``roofline``: every C3 matrix at every batch, kernel only where the API allows it (batch
+  1-8: kai_fused_mmvq with the activation prepared once outside the graph; batch 16:
+  kai_fused_mmq_run, whose operand preparation runs inside the call); weight bytes per launch
+  over the mean launch time. The headline fields are those of the dominant launch (the longest
+  kernel-only one), with its HBM traffic from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+  summary of that matrix.
 * ``legs``: every BASELINE config as whole calls (preparation included, as a caller sees
   them): C1, C2 and C5 decode, C3 per matrix and batch, C4 spec-verify (M=80, GB/s) and
   prefill (M=512, 2048, TOPS), C5 batch 16 and prefill. Each leg names its kernel.
@@ -112,6 +115,8 @@ def kernel_name(qtype, m, n, k):
         return "v_dot4 GEMV (mmvq_kernel)"
     if persistent(n):
         return "persistent paired int8 GEMM (mmqd_kernel)"
+    if (n + 15) // 16 < 512 and k >= 32 * 256:  # kai_mmq.cuh launch_mmq_type: K pieces
+        return "paired int8 MMQ tile with K pieces across workgroups (mmq_kernel, PAIR)"
     return "paired int8 MMQ tile (mmq_kernel, PAIR)"
 
 
@@ -258,34 +263,38 @@ def main():
     print(f"[bench] step {ms_step * 1e3:.1f} us for {step_bytes / 1e6:.1f} MB of weights", file=sys.stderr,
           flush=True)
 
-    # ---- roofline: Q4_K gate/up decode kernel alone (activation prepared outside the graph)
-    name, qtype, n, k = C3[0]
-    key = ("C3", name)
-    decode = [m for m in batches if m <= 8]
-    kernel_us = {}
-    for m in decode:
-        x = r.x[k][:m]
-        native.check(lib, lib.kai_fused_prepare(x.data_ptr(), 2, m, k, k, r.act[k].data_ptr(), 0,
-                                                torch.cuda.current_stream().cuda_stream))
-        torch.cuda.synchronize()
-        kernel_us[m] = r.per_launch_us(key, qtype, n, k, m, max(10, args.steps // 4), 2, prepare=False)
-    wb = weight_bytes(qtype, n, k)
-    avg_us = float(np.mean(list(kernel_us.values())))
-    achieved = wb / (avg_us * 1e-6) / 1e9
-    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+    # ---- roofline: every C3 launch, kernel only for the decode batches (activation prepared
+    # once outside the graph); batch 16 is a whole kai_fused_mmq_run call
+    by_launch = {}
+    for name, qtype, n, k in C3:
+        key = ("C3", name)
+        wb = weight_bytes(qtype, n, k)
+        for m in batches:
+            if m <= 8:
+                x = r.x[k][:m]
+                native.check(lib, lib.kai_fused_prepare(x.data_ptr(), 2, m, k, k, r.act[k].data_ptr(), 0,
+                                                        torch.cuda.current_stream().cuda_stream))
+                torch.cuda.synchronize()
+            us = r.per_launch_us(key, qtype, n, k, m, max(10, args.steps // 4), 2, prepare=False)
+            gbs = wb / (us * 1e-6) / 1e9
+            by_launch[f"{name} b{m}"] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                                         "kernel": kernel_name(qtype, m, n, k), "bytes": wb,
+                                         "timed": "kernel only" if m <= 8 else "whole call (preparation inside)"}
+    dom_name = max((kk for kk, v in by_launch.items() if v["timed"] == "kernel only"), key=lambda kk: by_launch[kk]["us"])
+    dom = by_launch[dom_name]
+    dmat, dm = dom_name.split(" b")
+    achieved = dom["GB/s"]
+    roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": f"Q4_K gate/up 34816x5120 decode kernel, batch {','.join(map(str, decode))} "
-                      "(GEMV up to 3 rows, persistent paired int8 GEMM above), activation prepared outside the timing",
-            "bytes_per_launch": wb, "avg_launch_us": round(avg_us, 2),
-            "by_batch": {str(m): {"us": round(u, 2), "GB/s": round(wb / (u * 1e-6) / 1e9, 1),
-                                  "kernel": kernel_name(qtype, m, n, k)} for m, u in kernel_us.items()}}
-    tfile = ROOT / "profiles" / "gemv_q4k_34816x5120_traffic.json"
+            "kernel": f"{dom_name}: {dom['kernel']} (the longest kernel-only launch of the step)",
+            "bytes_per_launch": dom["bytes"], "avg_launch_us": dom["us"], "by_launch": by_launch}
+    tfile = ROOT / "profiles" / f"decode_traffic_{dmat}.json"
     if tfile.exists():
         tb = json.loads(tfile.read_text()).get("by_batch", {})
-        if all(str(m) in tb for m in decode):
-            roof["traffic"] = round(float(np.mean([tb[str(m)]["bytes"] for m in decode])))
+        if dm in tb:
+            roof["traffic"] = tb[dm]["bytes"]
             roof["traffic_source"] = f"profiles/{tfile.name} (rocprofv3 FETCH_SIZE/WRITE_SIZE, not this run)"
-    print(f"[bench] roofline {roof['by_batch']}", file=sys.stderr, flush=True)
+    print(f"[bench] roofline {by_launch}", file=sys.stderr, flush=True)
 
     # ---- per-config legs: whole calls
     legs = []
