@@ -128,21 +128,30 @@ int kai_upload_rows(const char *path, int64_t file_offset, int64_t src_rows, int
                     const int64_t *block_order, void *dst, uintptr_t stream);
 
 /* GEMV: dst[j * stride_dst + r] = inverse[j] * sum_b dot(W[r, b], q8[j, b]) for
- * r < n, j < m <= 8; F32 or BF16 (dst_bf16) output.
+ * r < n, j < m <= 8; F32 or BF16 (dst_bf16) output. Takes no scratch; on long rows of
+ * matrices with few 16-row sets it splits K across workgroups through a library-owned
+ * device array of 4 slots rotated per launch, so at most 4 such launches may overlap on
+ * one GPU (more race).
  * Replaces kai_fused_mmvq (current_ggml_direct.cu:946-965; kernel kai_dual_mmvq.cuh:258-397). */
 int kai_fused_mmvq(const void *weight, int type, int64_t n, int64_t k, int64_t m,
                    const void *activation, int two_pass, void *dst, int dst_bf16,
                    int64_t stride_dst, uintptr_t stream);
 
 /* Scratch bytes kai_fused_mmq_run needs for `count` matrices (types[i], rows[i])
- * sharing k, at m > 8 activation rows: [inverse: m floats][one activation region per
- * layout the group reads, D4 then DS4 then D2S6][up to 16 rows: the small-M GEMM's fp32
- * partial sums, 16 x 16 values per piece of a 16-row set (a few pieces per set)], each
- * region padded to 256 bytes. Above 16 rows a region is a plane: 128-value blocks of 144 bytes in [k/128][m]
- * order with k padded to 512; up to 16 rows it is the same quantisation laid out for the
- * small-M GEMM's LDS, 4608 bytes (D4) or 5632 bytes (DS4, D2S6) per 256 values of k.
- * direct_f32 is accepted for signature compatibility (outputs are always stored in
- * place). Replaces kai_fused_mmq_workspace (current_ggml_direct.cu:1196-1205). */
+ * sharing k, at m > 8 activation rows: [inverse: m floats][one int8 activation region per
+ * layout read by a matrix on the int8 kernels, D4 then DS4 then D2S6][one fp16 image
+ * (codes, then min-pass sums) per layout read by a matrix on the fp16 GEMM][the fp32
+ * partial sums of a kernel that splits K], each region padded to 256 bytes. Up to 16 rows
+ * the int8 region is the small-M image (the GGML MMQ quantisation laid out for the small-M
+ * GEMM's LDS, 4608 bytes (D4) or 5632 bytes (DS4, D2S6) per 256 values of k) and the
+ * partial sums the small-M GEMM's (16 x 16 values per piece of a 16-row set). Above 16 rows
+ * a matrix runs on the fp16 GEMM when mmq_uses_h(type, m, rows) holds (every type but
+ * Q6_K, except more than 16384 rows up to 96 rows), reading the fp16 image: codes
+ * half(d * q) as [k padded to 256 / 16][m padded to 32][16], and per 256 values of k and row
+ * 64 (DS4) or 128 (D2S6) bytes of min-pass sums (none for D4); the others read a plane:
+ * 128-value blocks of 144 bytes in [k/128][m] order with k padded to 512. The size is not
+ * monotonic in m. direct_f32 is accepted for signature compatibility (outputs are always
+ * stored in place). Replaces kai_fused_mmq_workspace (current_ggml_direct.cu:1196-1205). */
 size_t kai_fused_mmq_workspace(int device, const int *types, const int64_t *rows, int count,
                                int64_t k, int64_t m, int direct_f32);
 
