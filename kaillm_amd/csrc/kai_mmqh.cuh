@@ -525,8 +525,13 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
 
     // ---- epilogue: lane (col, kh) holds activation row i = col of each activation tile and
     // weight rows 8 q + 4 kh + (0..3) of each weight tile; one branch per kind of output
+    // A lane's four consecutive weight rows of one activation row go out as one 16-byte (f32) or
+    // 8-byte (bf16) store where the row is aligned for it: a quarter of the store requests of
+    // element stores (Q4_K 34816 x 5120 at 2048 rows 1235 -> 1063 us, 5120 x 17408 818 -> 655 us).
     auto store_all = [&](auto kind_tag) __attribute__((always_inline)) {
         constexpr int KIND = decltype(kind_tag)::value;  // 0 partial sums, 1 f32, 2 bf16
+        const bool vec = KIND == 0 ? n % 4 == 0
+                                   : stride_dst % 4 == 0 && (reinterpret_cast<uintptr_t>(dst) & (KIND == 1 ? 15 : 7)) == 0;
 #pragma unroll
         for (int tm = 0; tm < WM; ++tm) {
             const int i = m0 + arow0 + 32 * tm + col;
@@ -540,6 +545,17 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int j0 = n0 + wrow0 + 32 * tn + 8 * q + 4 * kh;
+                    if (vec && j0 + 3 < n) {
+                        const float v0 = acc[tn][tm][4 * q] * inv, v1 = acc[tn][tm][4 * q + 1] * inv,
+                                    v2 = acc[tn][tm][4 * q + 2] * inv, v3 = acc[tn][tm][4 * q + 3] * inv;
+                        if constexpr (KIND == 2)
+                            *reinterpret_cast<uint2 *>(rowh + j0) =
+                                make_uint2(float_to_bf16_bits(v0) | (uint32_t(float_to_bf16_bits(v1)) << 16),
+                                           float_to_bf16_bits(v2) | (uint32_t(float_to_bf16_bits(v3)) << 16));
+                        else
+                            *reinterpret_cast<float4 *>(rowf + j0) = make_float4(v0, v1, v2, v3);
+                        continue;
+                    }
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         if (j0 + e < n) {

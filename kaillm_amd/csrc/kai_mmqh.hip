@@ -10,6 +10,42 @@ __global__ __launch_bounds__(256) void mmqh_reduce_kernel(const float *__restric
                                                           int64_t stride_dst, int dst_bf16) {
     const int64_t total = int64_t(m) * n;
     const int64_t e0 = (int64_t(blockIdx.x) * 256 + threadIdx.x) * 4;
+    if (n % 4 == 0) {  // the four elements share a row: 16-byte loads of every split, in split order
+        if (e0 >= total) return;
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int z = 0; z < splits; ++z) {
+            const float4 p = *reinterpret_cast<const float4 *>(partial + int64_t(z) * total + e0);
+            v.x += p.x;
+            v.y += p.y;
+            v.z += p.z;
+            v.w += p.w;
+        }
+        const int i = static_cast<int>(e0 / n), j = static_cast<int>(e0 % n);
+        const float inv = inverse[i];
+        v.x *= inv;
+        v.y *= inv;
+        v.z *= inv;
+        v.w *= inv;
+        const int64_t idx = int64_t(i) * stride_dst + j;
+        if (dst_bf16) {
+            const uint32_t lo = float_to_bf16_bits(v.x) | (uint32_t(float_to_bf16_bits(v.y)) << 16),
+                           hi = float_to_bf16_bits(v.z) | (uint32_t(float_to_bf16_bits(v.w)) << 16);
+            uint16_t *d = static_cast<uint16_t *>(dst) + idx;
+            if ((reinterpret_cast<uintptr_t>(d) & 7) == 0) {
+                *reinterpret_cast<uint2 *>(d) = make_uint2(lo, hi);
+            } else {
+                d[0] = lo & 0xffffu, d[1] = lo >> 16, d[2] = hi & 0xffffu, d[3] = hi >> 16;
+            }
+        } else {
+            float *d = static_cast<float *>(dst) + idx;
+            if ((reinterpret_cast<uintptr_t>(d) & 15) == 0) {
+                *reinterpret_cast<float4 *>(d) = v;
+            } else {
+                d[0] = v.x, d[1] = v.y, d[2] = v.z, d[3] = v.w;
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int64_t e = e0 + q;
