@@ -474,26 +474,12 @@ __device__ __forceinline__ uint32_t half_hi(float v) { return float_to_half_bits
 __device__ __forceinline__ uint32_t half_lo(float v) { return float_to_half_bits(v - half_bits_to_float(half_hi(v))); }
 
 // LEGACY: the legacy ops' quantisation (no row normalisation, inverse 1, legacy_mmq_lane).
-template <int DTYPE, bool LEGACY>
-__global__ __launch_bounds__(PREP_THREADS) void prepare_mmq_kernel(
-    const typename Src<DTYPE>::T *__restrict__ x, int64_t stride_x, int k, int m, int kpad_blocks, int hblocks, int mpad,
-    MmqPlanes p) {
-    __shared__ float wave_max_lds[PREP_THREADS / WAVE];
-    const int row = blockIdx.x;  // images: rows m..15 are written as zeros
-    const int nblocks = k / QK8_1;
-    const int part = threadIdx.x & 3, ib = blockIdx.y * PREP_BLOCKS + (threadIdx.x >> 2);
-    const auto *xr = x + static_cast<int64_t>(row) * stride_x;
-    float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    float scale = 0.0f;
-    if constexpr (LEGACY) {
-        if (row < m) {
-            if (blockIdx.y == 0 && threadIdx.x == 0) p.inverse[row] = 1.0f;
-            if (ib < nblocks) load8<DTYPE>(xr + QK8_1 * ib + 8 * part, v);
-            scale = 1.0f;
-        }
-    } else if (row < m) {  // uniform over the workgroup
-        scale = row_scale<DTYPE>(xr, k, wave_max_lds, p.inverse + row, blockIdx.y == 0 && threadIdx.x == 0, v);
-    }
+// One chunk's share of a lane: block ib of the row, values 8 part .. 8 part + 7 (v, before the
+// row scale), into every plane and image the group reads.
+template <bool LEGACY>
+__device__ __forceinline__ void prepare_mmq_chunk(const MmqPlanes &p, float (&v)[8], float scale, int ib, int row,
+                                                  int part, int k, int m, int nblocks, int kpad_blocks, int hblocks,
+                                                  int mpad) {
     if (ib >= kpad_blocks) return;  // whole groups of 8 lanes (kpad_blocks is a multiple of 16)
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = ib < nblocks ? v[j] * scale : 0.0f;
@@ -574,6 +560,39 @@ __global__ __launch_bounds__(PREP_THREADS) void prepare_mmq_kernel(
     }
 }
 
+template <int DTYPE, bool LEGACY>
+__global__ __launch_bounds__(PREP_THREADS) void prepare_mmq_kernel(
+    const typename Src<DTYPE>::T *__restrict__ x, int64_t stride_x, int k, int m, int kpad_blocks, int hblocks, int mpad,
+    MmqPlanes p, int chunks) {
+    __shared__ float wave_max_lds[PREP_THREADS / WAVE];
+    const int row = blockIdx.x;  // images: rows m..15 are written as zeros
+    const int nblocks = k / QK8_1;
+    const int part = threadIdx.x & 3;
+    const auto *xr = x + static_cast<int64_t>(row) * stride_x;
+    float own[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    float scale = 0.0f;
+    if constexpr (LEGACY) {
+        if (row < m && blockIdx.y == 0 && threadIdx.x == 0) p.inverse[row] = 1.0f;
+        scale = 1.0f;
+    } else if (row < m) {  // uniform over the workgroup
+        scale = row_scale<DTYPE>(xr, k, wave_max_lds, p.inverse + row, blockIdx.y == 0 && threadIdx.x == 0, own);
+    }
+    // chunks of PREP_BLOCKS blocks: the workgroup's first from the row maximum's pass (own), the
+    // others read again (from L2)
+    for (int c = 0; c < chunks; ++c) {
+        const int ib = (blockIdx.y * chunks + c) * PREP_BLOCKS + (threadIdx.x >> 2);
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = own[j];
+        if (LEGACY || c > 0) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = 0.0f;
+            if (row < m && ib < nblocks) load8<DTYPE>(xr + QK8_1 * ib + 8 * part, v);
+        }
+        prepare_mmq_chunk<LEGACY>(p, v, scale, ib, row, part, k, m, nblocks, kpad_blocks, hblocks, mpad);
+    }
+}
+
 template <int DTYPE>
 static void launch_prepare_dtype(const void *x, int64_t m, int64_t k, int64_t stride_x, const ActLayout &o,
                                  hipStream_t stream) {
@@ -608,14 +627,18 @@ static void launch_prepare_mmq_dtype(const void *x, int64_t m, int64_t k, int64_
     // images: the zero rows too (small-M images to 16 rows, fp16 images to mmqh_mpad(m))
     const int64_t rows = p.image ? MMQS_MAX_ROWS : any_h ? mmqh_mpad(m) : m;
     const int hblocks = static_cast<int>(mmqh_kpad(k) / QK8_1), mpad = static_cast<int>(mmqh_mpad(m));
-    const dim3 grid(static_cast<unsigned>(rows), static_cast<unsigned>((kpad_blocks + PREP_BLOCKS - 1) / PREP_BLOCKS));
+    // Many rows: one workgroup per row walks all its chunks, so the row maximum is read once per
+    // row instead of once per chunk (at 2048 rows of K = 17408, nine times)
+    const int all_chunks = (kpad_blocks + PREP_BLOCKS - 1) / PREP_BLOCKS;
+    const int chunks = rows >= 256 ? all_chunks : 1;
+    const dim3 grid(static_cast<unsigned>(rows), static_cast<unsigned>((all_chunks + chunks - 1) / chunks));
     const auto *src = static_cast<const typename Src<DTYPE>::T *>(x);
     if (p.legacy)
         prepare_mmq_kernel<DTYPE, true><<<grid, dim3(PREP_THREADS), 0, stream>>>(
-            src, stride_x, static_cast<int>(k), static_cast<int>(m), kpad_blocks, hblocks, mpad, p);
+            src, stride_x, static_cast<int>(k), static_cast<int>(m), kpad_blocks, hblocks, mpad, p, chunks);
     else
         prepare_mmq_kernel<DTYPE, false><<<grid, dim3(PREP_THREADS), 0, stream>>>(
-            src, stride_x, static_cast<int>(k), static_cast<int>(m), kpad_blocks, hblocks, mpad, p);
+            src, stride_x, static_cast<int>(k), static_cast<int>(m), kpad_blocks, hblocks, mpad, p, chunks);
 }
 
 void launch_prepare_mmq(const void *x, int x_dtype, int64_t m, int64_t k, int64_t stride_x, const MmqPlanes &planes,
