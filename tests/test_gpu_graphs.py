@@ -5,8 +5,9 @@ projection, a SwiGLU down projection and a projection read through an input view
 the batched path (the small-M, persistent and tiled GEMMs with their scratch) are captured once,
 then replayed with new inputs written into the captured buffers. Between replays the same
 step runs eagerly on the same inputs, and every replay must equal it bit for bit (the
-kernels have fixed reduction orders and no atomics). The library issues no memset and no
-allocation of its own; torch's graph pool holds every buffer.
+kernels have fixed reduction orders; the decode tile's K pieces count their arrivals with
+atomics but add the pieces in K order). The library issues no memset and no allocation of its
+own; torch's graph pool holds every buffer.
 """
 import numpy as np
 import pytest
@@ -83,6 +84,53 @@ def test_decode_step_graph_replays_equal_eager(kai, m, monkeypatch):
         assert native_fused.CONSUMER_OF  # the qkv consumer was registered for the producer
     for replay in range(3):
         fill(10 + replay)
+        eager = [t.clone() for t in step()]
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, want in zip(static_out, eager):
+            assert torch.equal(got, want), f"replay {replay}"
+    del graph
+
+
+@pytest.mark.parametrize("m", [5, 8])
+def test_decode_k_pieces_graph_replays_equal_eager(kai, m):
+    """Two decode projections whose tiled paired kernel splits K across workgroups (320 row
+    sets of long rows) captured in one graph: each launch took its slot of partial sums at
+    capture, and every replay, with eager calls of the same projections in between, must
+    equal the eager result bit for bit (the arrival counts are back at zero after each
+    launch)."""
+    from kaillm_amd.linear import GGUFLinearMethod
+
+    print(f"graph K pieces m={m}", flush=True)
+    rng = np.random.default_rng(950 + m)
+    k = 8192
+    method = GGUFLinearMethod()
+    first = _layer([(O.Q6_K, O.random_blocks(O.Q6_K, 5120, k, rng))])
+    second = _layer([(O.Q6_K, O.random_blocks(O.Q6_K, 5120, k, rng))])
+    x = torch.empty((m, k), dtype=torch.bfloat16, device=DEV)
+
+    def step():
+        return [method.apply(first, x), method.apply(second, x)]
+
+    def fill(seed):
+        g = np.random.default_rng(seed)
+        x.copy_(to_dev(g.standard_normal((m, k)).astype(np.float32)).to(torch.bfloat16))
+
+    fill(1)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out = step()
+    torch.cuda.synchronize()
+    for replay in range(3):
+        fill(20 + replay)
         eager = [t.clone() for t in step()]
         torch.cuda.synchronize()
         graph.replay()
