@@ -309,6 +309,50 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
     using J2 = std::integral_constant<int, 2>;
     using J3 = std::integral_constant<int, 3>;
 
+    // Weight conversion of stage s into wb from raw LDS, by either role: thread ctid of the
+    // producers or of the compute waves converts the same units. The producers convert the
+    // stages that start a superblock's halves (even stages, with the superblock's min-pass
+    // factors at its first), the compute waves the odd stages in the time they would otherwise
+    // spend at the barrier (their MFMAs are still in the pipe; the conversion reads only LDS).
+    const int ctid = wave >= CW ? tid - THREADS : tid;
+    // weights: unit u = h * BN + j (32 values of row j: half h of a stage)
+    // first: s is a superblock's first stage (its min-pass factors go to WMIN)
+    auto wstore = [&](int s, lds_u8 *wb, auto first) __attribute__((always_inline)) {
+        const lds_u8 *rb = ((s >> 2) & 1) ? R1 : R0;
+        const int valid = SHORT ? k / QK8_1 - 8 * (s >> 2) : 8;  // blocks of the step in the row
+#pragma unroll
+        for (int p = 0; p < UPT; ++p) {
+            const int u = ctid + p * THREADS, j = u % BN, h = u / BN;
+            uint4 c[4];
+            W::convert(rb + j * W::RS, s & 3, h, valid, grid_lds, c);
+            store16(wb + (2 * h) * BN * 32 + mmqh_swz(j, 0), c[0]);
+            store16(wb + (2 * h) * BN * 32 + mmqh_swz(j, 1), c[1]);
+            store16(wb + (2 * h + 1) * BN * 32 + mmqh_swz(j, 0), c[2]);
+            store16(wb + (2 * h + 1) * BN * 32 + mmqh_swz(j, 1), c[3]);
+            if constexpr (W::C0 != 0) {
+                if constexpr (decltype(first)::value) {
+                    uint4 o0, o1;
+                    W::mins(rb + j * W::RS, h, o0, o1);
+                    store16(wmin + j * 64 + 32 * h, o0);
+                    store16(wmin + j * 64 + 32 * h + 16, o1);
+                }
+            }
+        }
+    };
+    // the min-pass factors of stage s's superblock (s its first stage) into WMIN
+    auto wmins = [&](int s) __attribute__((always_inline)) {
+        if constexpr (W::C0 != 0) {
+            const lds_u8 *rb = ((s >> 2) & 1) ? R1 : R0;
+#pragma unroll
+            for (int p = 0; p < UPT; ++p) {
+                const int u = ctid + p * THREADS, j = u % BN, h = u / BN;
+                uint4 o0, o1;
+                W::mins(rb + j * W::RS, h, o0, o1);
+                store16(wmin + j * 64 + 32 * h, o0);
+                store16(wmin + j * 64 + 32 * h + 16, o1);
+            }
+        }
+    };
     if (wave >= CW) {
         // ================= producer waves
         const int ptid = tid - THREADS;
@@ -341,30 +385,6 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
             for (int p = 0; p < RPT; ++p)
                 if (RAWC % THREADS == 0 || ptid + p * THREADS < RAWC) store_unaligned(rb + raw_at[p] + raw_off[p], rawv[p]);
-        };
-        // weights: unit u = h * BN + j (32 values of row j: half h of a stage)
-        // first: s is a superblock's first stage (its min-pass factors go to WMIN)
-        auto wstore = [&](int s, lds_u8 *wb, auto first) __attribute__((always_inline)) {
-            const lds_u8 *rb = ((s >> 2) & 1) ? R1 : R0;
-            const int valid = SHORT ? nblocks - 8 * (s >> 2) : 8;  // blocks of the step in the row
-#pragma unroll
-            for (int p = 0; p < UPT; ++p) {
-                const int u = ptid + p * THREADS, j = u % BN, h = u / BN;
-                uint4 c[4];
-                W::convert(rb + j * W::RS, s & 3, h, valid, grid_lds, c);
-                store16(wb + (2 * h) * BN * 32 + mmqh_swz(j, 0), c[0]);
-                store16(wb + (2 * h) * BN * 32 + mmqh_swz(j, 1), c[1]);
-                store16(wb + (2 * h + 1) * BN * 32 + mmqh_swz(j, 0), c[2]);
-                store16(wb + (2 * h + 1) * BN * 32 + mmqh_swz(j, 1), c[3]);
-                if constexpr (W::C0 != 0) {
-                    if constexpr (decltype(first)::value) {
-                        uint4 o0, o1;
-                        W::mins(rb + j * W::RS, h, o0, o1);
-                        store16(wmin + j * 64 + 32 * h, o0);
-                        store16(wmin + j * 64 + 32 * h + 16, o1);
-                    }
-                }
-            }
         };
         // activation: per stage, the image's 16-byte chunks (4 groups x BM rows x 32 bytes; chunk
         // w of a group holds row w / 2, half (w % 2) swizzled), loaded two stages ahead (ring of
@@ -420,7 +440,11 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
             aload(sl, vload);
             astore(vstore, anext);
             if constexpr (MIN_PW > 0 && J == 3) mstore();
-            wstore(sw, wnext, std::integral_constant<bool, J == 3>{});
+            // the next superblock's min-pass factors a stage before its first conversion (the
+            // compute waves read WMIN at each superblock's first stage only)
+            if constexpr (J == 2) wmins(min(s + 2, last) / 4 * 4);
+            if constexpr (J == 1 || J == 3) wstore(sw, wnext, std::false_type{});
+            (void)wnext;
             mmqh_barrier();
         };
         if constexpr (TYPE == IQ3_S) mmqh_barrier();  // the grid, before the first conversion
@@ -465,7 +489,8 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
     // within a group the tiles' MFMAs are independent.
     const int wrow0 = wn * 32 * WN, arow0 = wm * 32 * WM;
     const int a_off = mmqh_swz(wrow0 + col, kh), b_off = mmqh_swz(arow0 + col, kh);
-    auto compute = [&](const lds_u8 *ab, const lds_u8 *wb, auto first) __attribute__((always_inline)) {
+    auto compute = [&](const lds_u8 *ab, const lds_u8 *wb, auto first, int sconv, lds_u8 *wconv)
+                       __attribute__((always_inline)) {
         v8h_t a[4][WN], b[4][WM];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -509,6 +534,7 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
                                                                              bm[q][tm], acc[tn][tm], 0, 0, 0);
           }
         }
+        if (wconv) wstore(sconv, wconv, std::false_type{});
         mmqh_barrier();
     };
     if constexpr (TYPE == IQ3_S) mmqh_barrier();
@@ -516,10 +542,10 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
         mmqh_barrier();  // the producers' wire bytes of the first step
         mmqh_barrier();  // and its first stage
         for (int s = s0; s < s1; s += 4) {
-            compute(A0, W0, std::true_type{});
-            compute(A1, W1, std::false_type{});
-            compute(A0, W0, std::false_type{});
-            compute(A1, W1, std::false_type{});
+            compute(A0, W0, std::true_type{}, min(s + 1, last), W1);
+            compute(A1, W1, std::false_type{}, 0, nullptr);
+            compute(A0, W0, std::false_type{}, min(s + 3, last), W1);
+            compute(A1, W1, std::false_type{}, 0, nullptr);
         }
     }
 
