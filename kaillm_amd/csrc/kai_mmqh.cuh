@@ -20,12 +20,13 @@
 // .. +8; result: column l % 32, rows 8 * (r / 4) + 4 * (l / 32) + r % 4 for r = 0..15.
 //
 // Workgroup: 2 * GN * GM waves. The first GN * GM compute: each owns WN x WM tiles of 32 x 32,
-// BN = 32 WN GN weight rows by BM = 32 WM GM activation rows, and only reads LDS and runs
-// MFMAs. The other GN * GM produce: they load the activation image and the weights' wire bytes
-// and convert the weights. Waves w and w + GN GM share a SIMD (waves are dealt to the 4 SIMDs in
-// turn), so each SIMD runs one of each and the producer's VALU work overlaps the MFMAs. (A
-// compute wave that also converted would read MFMA results on the VALU or wait on memory in
-// the middle of its MFMA stream; either stalls the stream.)
+// BN = 32 WN GN weight rows by BM = 32 WM GM activation rows; they read their operands from LDS
+// and run MFMAs, and, after issuing a stage's MFMAs, convert every other stage's weights from
+// raw LDS (no global memory and no MFMA result is touched, so the MFMA stream does not stall,
+// and the conversion fills time the wave would spend at the barrier). The other GN * GM
+// produce: they load the activation image and the weights' wire bytes and convert the other
+// stages' weights and each superblock's min-pass factors. Waves w and w + GN GM share a SIMD
+// (waves are dealt to the 4 SIMDs in turn), so each SIMD runs one of each.
 //
 // K runs in stages of 64 values (4 groups of 16), 4 stages a step (256 values, one superblock).
 // LDS, static arrays:
@@ -40,8 +41,10 @@
 // Stage s, between two s_barriers:
 //   producers: load stage s + 3's activation chunks (ring of 4 stages in registers) and write
 //     stage s + 1's; at a step's first stage, write step i + 1's wire bytes (loaded a step
-//     earlier) to raw LDS and load step i + 2's; convert stage s + 1's weights from raw LDS;
-//   compute: stage s's MFMAs from LDS stage s % 2, at a step's first stage also the min pass.
+//     earlier) to raw LDS and load step i + 2's; convert stage s + 1's weights from raw LDS when
+//     s + 1 is even; at a step's third stage, the next superblock's min-pass factors (WMIN);
+//   compute: stage s's MFMAs from LDS stage s % 2, at a step's first stage also the min pass;
+//     then convert stage s + 1's weights when s + 1 is odd.
 // The barrier is a bare s_barrier after lgkmcnt(0) (a memory fence would wait for every load in
 // flight). Every global load is issued unconditionally, clamped to the split's last stage at its
 // end, so that the compiler's count of loads in flight stays exact and each wait is for the
