@@ -20,7 +20,9 @@ working set.
   summary of that matrix.
 * ``legs``: every BASELINE config as whole calls (preparation included, as a caller sees
   them): C1, C2 and C5 decode, C3 per matrix and batch, C4 spec-verify (M=80, GB/s) and
-  prefill (M=512, 2048, TOPS), C5 batch 16 and prefill. Each leg names its kernel.
+  prefill (M=512, 2048, TOPS), C5 batch 16 and prefill. Each leg names its kernel. TOPS count
+  2·M·N·K ops; ``frac`` is against the dense int8 MFMA peak the target is set on, and the legs on
+  the folded fp16 GEMM also give ``fp16_frac``, against the fp16 MFMA peak of the pipe they use.
 * ``cpu_baseline``: the oracle (the C restatement of the reference arithmetic) on a bounded
   sample, on the host cores, with the CPU model and thread count.
 """
@@ -39,6 +41,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+FP16_PEAK_TFLOPS = 2500.0
 ROTATION_BYTES = 600e6   # weight copies per matrix: at least this many bytes in rotation
 MIN_COPIES = 3
 
@@ -307,6 +310,8 @@ def main():
         if m >= 512:
             tops = 2.0 * m * n * k / (us * 1e-6) / 1e12
             entry.update({"TOPS": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4), "bound": "mfma int8"})
+            if "fp16" in entry["kernel"]:
+                entry.update({"fp16_frac": round(tops / FP16_PEAK_TFLOPS, 4), "bound": "mfma fp16"})
         else:
             gbs = wbytes / (us * 1e-6) / 1e9
             entry.update({"GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "bound": "hbm"})
