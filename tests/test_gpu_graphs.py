@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import _oracle as O
-from test_gpu_parity import DEV, to_dev
+from test_gpu_parity import DEV, TOL_BF16, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -137,4 +137,58 @@ def test_decode_k_pieces_graph_replays_equal_eager(kai, m):
         torch.cuda.synchronize()
         for got, want in zip(static_out, eager):
             assert torch.equal(got, want), f"replay {replay}"
+    del graph
+
+
+@pytest.mark.parametrize("m", [9, 16])
+def test_small_m_pieces_graph_replays_equal_eager(kai, m):
+    """The small-M GEMM on long and short Q6_K rows (5120 x 17408 and 5120 x 6144, the C3 down
+    and o_proj shapes), whose row sets are cut into pieces across waves and workgroups and
+    added by its reduction launch: captured in one graph, every replay, with eager calls in
+    between, must equal the eager result bit for bit, and the eager result must match the
+    oracle."""
+    from kaillm_amd.linear import GGUFLinearMethod
+
+    print(f"graph small-M pieces m={m}", flush=True)
+    rng = np.random.default_rng(970 + m)
+    method = GGUFLinearMethod()
+    shapes = [(5120, 17408), (5120, 6144)]
+    parts = [O.random_blocks(O.Q6_K, n, k, rng) for n, k in shapes]
+    layers = [_layer([(O.Q6_K, w)], torch.float16) for w in parts]
+    xs = [torch.empty((m, k), dtype=torch.float16, device=DEV) for _, k in shapes]
+
+    def step():
+        return [method.apply(layer, x) for layer, x in zip(layers, xs)]
+
+    def fill(seed):
+        g = np.random.default_rng(seed)
+        for x in xs:
+            x.copy_(to_dev(g.standard_normal(tuple(x.shape)).astype(np.float32)).to(torch.float16))
+
+    fill(1)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out = step()
+    torch.cuda.synchronize()
+    for replay in range(3):
+        fill(30 + replay)
+        eager = [t.clone() for t in step()]
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, want in zip(static_out, eager):
+            assert torch.equal(got, want), f"replay {replay}"
+    cols = np.arange(0, 5120, 37)
+    for w, (n, k), x, got in zip(parts, shapes, xs, eager):
+        want = O.mmq_reference(O.Q6_K, w[cols], x.cpu().numpy(), threads=16)
+        err = O.normwise_rel(got.float().cpu().numpy()[:, cols], want)
+        print(f"  {n}x{k} normwise rel err {err:.3e}")
+        assert err <= TOL_BF16  # the projection writes bf16 for a 16-bit layer
     del graph
