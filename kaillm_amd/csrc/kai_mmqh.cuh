@@ -24,31 +24,35 @@
 // and run MFMAs, and, after issuing a stage's MFMAs, convert every other stage's weights from
 // raw LDS (no global memory and no MFMA result is touched, so the MFMA stream does not stall,
 // and the conversion fills time the wave would spend at the barrier). The other GN * GM
-// produce: they load the activation image and the weights' wire bytes and convert the other
-// stages' weights and each superblock's min-pass factors. Waves w and w + GN GM share a SIMD
+// produce: they copy the activation image into LDS, load the weights' wire bytes and convert
+// the other stages' weights and each superblock's min-pass factors. Waves w and w + GN GM share a SIMD
 // (waves are dealt to the 4 SIMDs in turn), so each SIMD runs one of each.
 //
 // K runs in stages of 64 values (4 groups of 16), 4 stages a step (256 values, one superblock).
 // LDS, static arrays:
 //   * 2 activation stages, the codes [group 4][BM rows][32 B];
 //   * 2 weight stages, the folded codes [4][BN][32 B];
-//   * 2 raw weight steps, each row's wire bytes of one step [BN][RS] (copied 16 bytes a lane,
-//     consecutive lanes along a row, so that a wave's loads touch few cache lines);
+//   * 2 raw weight steps (one array), each row's wire bytes of one step [BN][RS] (copied 16
+//     bytes a lane, consecutive lanes along a row, so that a wave's loads touch few cache lines);
 //   * the current superblock's min-pass operands, WMIN [BN][64 B] and AMIN [BM][AB].
 // In the code blocks the two 16-byte halves of row r are exchanged when bit 2 of r differs from
 // bit 3 (mmqh_swz): 8 or 16 lanes reading consecutive rows then hit distinct banks.
 //
 // Stage s, between two s_barriers:
-//   producers: load stage s + 3's activation chunks (ring of 4 stages in registers) and write
-//     stage s + 1's; at a step's first stage, write step i + 1's wire bytes (loaded a step
-//     earlier) to raw LDS and load step i + 2's; convert stage s + 1's weights from raw LDS when
-//     s + 1 is even; at a step's third stage, the next superblock's min-pass factors (WMIN);
+//   producers: copy stage s + 1's activation chunks from global memory straight into LDS
+//     (global_load_lds_dwordx4, no registers) and wait for them at the stage's end; at a step's
+//     first stage, write step i + 1's wire bytes (loaded a step earlier) to raw LDS and load
+//     step i + 2's; convert stage s + 1's weights from raw LDS when s + 1 is even; at a step's
+//     third stage, the next superblock's min-pass factors (WMIN);
 //   compute: stage s's MFMAs from LDS stage s % 2, at a step's first stage also the min pass;
 //     then convert stage s + 1's weights when s + 1 is odd.
 // The barrier is a bare s_barrier after lgkmcnt(0) (a memory fence would wait for every load in
 // flight). Every global load is issued unconditionally, clamped to the split's last stage at its
-// end, so that the compiler's count of loads in flight stays exact and each wait is for the
-// loads of two stages (wire bytes: a step) before.
+// end. Loads complete in issue order for the wait counter: the wire bytes and min-pass operands
+// are loaded after the stage's copies, so the wait for the copies leaves them in flight. The
+// register ring this replaced (activation loaded three stages ahead into registers, then
+// written to LDS) was 5-11 % slower at 512-2048 rows: the producers' LDS writes and their waits
+// were part of every stage.
 // Rows past the activation image and past the matrix are clamped; their outputs are never
 // stored. Split-K (grid.y > 1): each split writes its fp32 sums to scratch and
 // mmqh_reduce_kernel adds them in split order.
@@ -258,6 +262,13 @@ struct MmqhLds {
 // byte of 16-byte half h of row r within a group's [rows][32 B] block
 __host__ __device__ constexpr int mmqh_swz(int r, int h) { return 32 * r + 16 * (h ^ (((r >> 2) ^ (r >> 3)) & 1)); }
 
+// all but this wave's last N vector-memory loads are done (the global-to-LDS copies before them
+// have written the LDS)
+template <int N>
+__device__ __forceinline__ void mmqh_wait_loads() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
+}
 // this wave's LDS writes are done, then every wave of the workgroup meets (no fence)
 __device__ __forceinline__ void mmqh_barrier() {
     __builtin_amdgcn_sched_barrier(0);
@@ -282,14 +293,15 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
     __shared__ __align__(16) uint8_t act_lds1[L::ASTAGE];
     __shared__ __align__(16) uint8_t wt_lds0[L::WSTAGE];
     __shared__ __align__(16) uint8_t wt_lds1[L::WSTAGE];
-    __shared__ __align__(16) uint8_t raw_lds0[L::RAW];
-    __shared__ __align__(16) uint8_t raw_lds1[L::RAW];
+    __shared__ __align__(16) uint8_t raw_lds[2 * L::RAW];  // one array: its two halves by offset
     __shared__ __align__(16) uint8_t wmin_lds[L::WMIN];
     __shared__ __align__(16) uint8_t amin_lds[L::AMIN];
     __shared__ uint32_t grid_lds[TYPE == IQ3_S ? 512 : 1];
     lds_u8 *const A0 = (lds_u8 *)act_lds0, *const A1 = (lds_u8 *)act_lds1;
     lds_u8 *const W0 = (lds_u8 *)wt_lds0, *const W1 = (lds_u8 *)wt_lds1;
-    lds_u8 *const R0 = (lds_u8 *)raw_lds0, *const R1 = (lds_u8 *)raw_lds1;
+    // the raw step of step i (the compiler then sees every access's array, and so that the
+    // activation's global-to-LDS copies cannot touch the other buffers)
+    auto raw_of = [&](int i) __attribute__((always_inline)) { return (lds_u8 *)raw_lds + (i & 1) * L::RAW; };
     lds_u8 *const wmin = (lds_u8 *)wmin_lds, *const amin = (lds_u8 *)amin_lds;
 
     const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
@@ -321,7 +333,7 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
     // weights: unit u = h * BN + j (32 values of row j: half h of a stage)
     // first: s is a superblock's first stage (its min-pass factors go to WMIN)
     auto wstore = [&](int s, lds_u8 *wb, auto first) __attribute__((always_inline)) {
-        const lds_u8 *rb = ((s >> 2) & 1) ? R1 : R0;
+        const lds_u8 *rb = raw_of(s >> 2);
         const int valid = SHORT ? k / QK8_1 - 8 * (s >> 2) : 8;  // blocks of the step in the row
 #pragma unroll
         for (int p = 0; p < UPT; ++p) {
@@ -345,7 +357,7 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
     // the min-pass factors of stage s's superblock (s its first stage) into WMIN
     auto wmins = [&](int s) __attribute__((always_inline)) {
         if constexpr (W::C0 != 0) {
-            const lds_u8 *rb = ((s >> 2) & 1) ? R1 : R0;
+            const lds_u8 *rb = raw_of(s >> 2);
 #pragma unroll
             for (int p = 0; p < UPT; ++p) {
                 const int u = ctid + p * THREADS, j = u % BN, h = u / BN;
@@ -405,14 +417,22 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
         }
 #pragma unroll
         for (int p = 0; p < MIN_PW; ++p) min_src[p] = 16 * min(ptid + p * THREADS, rows_here * AB / 16 - 1);
-        auto aload = [&](int s, uint4 (&v)[CODE_PW]) __attribute__((always_inline)) {
+        // stage s's chunks straight into LDS (global_load_lds_dwordx4: a wave's 64 lanes fill
+        // 1 KiB in lane order at the wave-uniform LDS address in M0; no registers, no LDS
+        // write). Written as an asm statement: the compiler would otherwise make every later
+        // LDS read of this wave that it cannot tell apart from the copy wait for it. Nothing
+        // else in the kernel uses M0. The compiler does not count these loads, so its own waits
+        // for the loads issued before them wait longer, never shorter; the stage's waits for
+        // the copies are explicit (mmqh_wait_loads).
+        const int pwave = __builtin_amdgcn_readfirstlane(ptid / WAVE);
+        auto adma = [&](int s, lds_u8 *ab) __attribute__((always_inline)) {
             const uint8_t *cb = img.codes + (int64_t(4 * s) * img.mpad + m0) * 32;
 #pragma unroll
-            for (int p = 0; p < CODE_PW; ++p) v[p] = *reinterpret_cast<const uint4 *>(cb + code_src[p]);
-        };
-        auto astore = [&](const uint4 (&v)[CODE_PW], lds_u8 *ab) __attribute__((always_inline)) {
-#pragma unroll
-            for (int p = 0; p < CODE_PW; ++p) store16(ab + 16 * (ptid + p * THREADS), v[p]);
+            for (int p = 0; p < CODE_PW; ++p) {
+                const uint32_t la = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ab + 16 * (p * THREADS + WAVE * pwave)));
+                asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                             :: "s"(la), "v"(cb + code_src[p]) : "memory", "m0");
+            }
         };
         uint4 mv[MIN_PW > 0 ? MIN_PW : 1];
         auto mload = [&](int s) __attribute__((always_inline)) {  // s: a superblock's first stage
@@ -425,52 +445,51 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
             for (int p = 0; p < MIN_PW; ++p)
                 if (MIN_CH % THREADS == 0 || ptid + p * THREADS < MIN_CH) store16(amin + 16 * (ptid + p * THREADS), mv[p]);
         };
-        uint4 v0[CODE_PW], v1[CODE_PW], v2[CODE_PW], v3[CODE_PW];
-        // stage J of a step i (s = 4 i + J): load stage s + 3 into ring entry (J + 3) % 4, write
-        // stage s + 1 from entry (J + 1) % 4; the min-pass operands of a superblock are loaded
-        // with its first stage (J = 1 loads stage s + 3 = 4 i + 4) and written with it (J = 3
-        // writes stage s + 1); at J = 0 the wire bytes of step i + 1 (loaded at step i - 1) go
-        // to raw LDS and those of step i + 2 are loaded
-        auto pstep = [&](int s, auto jtag, lds_u8 *anext, lds_u8 *wnext, uint4 (&vload)[CODE_PW],
-                         const uint4 (&vstore)[CODE_PW]) __attribute__((always_inline)) {
+        // stage J of a step i (s = 4 i + J): copy stage s + 1's activation into LDS first; the
+        // min-pass operands of a superblock are loaded two stages before its first stage (J = 1)
+        // and written a stage before it (J = 3); at J = 0 the wire bytes of step i + 1 (loaded
+        // at step i - 1) go to raw LDS and those of step i + 2 are loaded. Loads complete in
+        // issue order for the wait counter, so the wait for the stage's copies before the
+        // barrier leaves the loads issued after them in flight.
+        auto pstep = [&](int s, auto jtag, lds_u8 *anext, lds_u8 *wnext) __attribute__((always_inline)) {
             constexpr int J = decltype(jtag)::value;
-            const int sl = min(s + 3, last), sw = min(s + 1, last), step = s >> 2;
-            if constexpr (J == 0) {
-                rstore(((step + 1) & 1) ? R1 : R0);
-                rload(min(step + 2, last >> 2));
-            }
-            if constexpr (MIN_PW > 0 && J == 1) mload(sl / 4 * 4);
-            aload(sl, vload);
-            astore(vstore, anext);
+            const int sw = min(s + 1, last), step = s >> 2;
+            // the register stores first: their waits then cover only the copies of earlier stages
+            if constexpr (J == 0) rstore(raw_of(step + 1));
             if constexpr (MIN_PW > 0 && J == 3) mstore();
+            __builtin_amdgcn_sched_barrier(0);
+            adma(sw, anext);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (J == 0) rload(min(step + 2, last >> 2));
+            if constexpr (MIN_PW > 0 && J == 1) mload(min(s + 3, last) / 4 * 4);
             // the next superblock's min-pass factors a stage before its first conversion (the
             // compute waves read WMIN at each superblock's first stage only)
             if constexpr (J == 2) wmins(min(s + 2, last) / 4 * 4);
             if constexpr (J == 1 || J == 3) wstore(sw, wnext, std::false_type{});
             (void)wnext;
+            __builtin_amdgcn_sched_barrier(0);
+            mmqh_wait_loads<(J == 0 ? RPT : 0) + (J == 1 ? MIN_PW : 0)>();
             mmqh_barrier();
         };
         if constexpr (TYPE == IQ3_S) mmqh_barrier();  // the grid, before the first conversion
         if (s0 < s1) {
-            // the loads in the loop's order (wire bytes, then the activation stages), so that the
-            // compiler's count of loads in flight at the loop's head agrees with the loop's own
             rload(s0 >> 2);
-            rstore(((s0 >> 2) & 1) ? R1 : R0);
-            rload(min((s0 >> 2) + 1, last >> 2));
+            rstore(raw_of(s0 >> 2));
             if constexpr (MIN_PW > 0) mload(s0);
-            aload(s0, v0);
-            aload(min(s0 + 1, last), v1);
-            aload(min(s0 + 2, last), v2);
+            adma(s0, A0);
+            __builtin_amdgcn_sched_barrier(0);
+            rload(min((s0 >> 2) + 1, last >> 2));
             if constexpr (MIN_PW > 0) mstore();
-            astore(v0, A0);
-            mmqh_barrier();  // the wire bytes of the first step
+            __builtin_amdgcn_sched_barrier(0);
+            mmqh_wait_loads<RPT>();
+            mmqh_barrier();  // the wire bytes of the first step, its activation and min operands
             wstore(s0, W0, std::true_type{});
             mmqh_barrier();
             for (int s = s0; s < s1; s += 4) {
-                pstep(s, J0{}, A1, W1, v3, v1);
-                pstep(s + 1, J1{}, A0, W0, v0, v2);
-                pstep(s + 2, J2{}, A1, W1, v1, v3);
-                pstep(s + 3, J3{}, A0, W0, v2, v0);
+                pstep(s, J0{}, A1, W1);
+                pstep(s + 1, J1{}, A0, W0);
+                pstep(s + 2, J2{}, A1, W1);
+                pstep(s + 3, J3{}, A0, W0);
             }
         }
         return;
