@@ -107,7 +107,7 @@ def parse():
 
 def kernel_name(qtype, m, n, k):
     if m > 16:
-        if qtype in (Q4_K, Q4_0, Q8_0, IQ3_S, Q2_K) and (m > 96 or n <= 16384):  # kai_launch.h mmq_uses_h
+        if qtype in (Q4_K, Q4_0, Q8_0, IQ3_S, Q2_K):  # kai_launch.h mmq_uses_h
             return "fp16 folded-operand GEMM (kai_fused_mmq_run: fp16 image + mmqh_kernel)"
         return "int8 MMQ (kai_fused_mmq_run: GGML MMQ planes + mmq_kernel)"
     if m > 8:

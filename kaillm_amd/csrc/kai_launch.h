@@ -212,12 +212,13 @@ struct MmqPlanes {
     MmqhImage h[3] = {};  // the fp16 GEMM's images per layout (null codes when not read)
 };
 // Whether kai_fused_mmq_run's m-row product of an n-row matrix with this type runs on the fp16
-// GEMM (reading the layout's fp16 image) rather than the int8 kernels (reading the plane). Up to
-// 96 rows a matrix of more than 16384 rows stays on the int8 tile kernel: its 272-and-more weight
-// tiles of 128 rows leave the fp16 GEMM's one workgroup per CU a partial second round (measured
-// at 80 rows on 34816 x 5120 Q4_K: 111 us int8, 144 us fp16; 5120-row matrices: 90 / 63 us).
+// GEMM (reading the layout's fp16 image) rather than the int8 kernels (reading the plane): above
+// 16 rows, every format but Q6_K. Measured at 80 rows (whole calls): Q4_K 34816 x 5120 111.7 us
+// on the int8 tile kernel, 107.0 us on the fp16 GEMM; 5120 x 17408 90 / 53 us. (n is the
+// matrix's rows, for the rule's callers.)
 inline bool mmq_uses_h(int type, int64_t m, int64_t n) {
-    return m > MMQS_MAX_ROWS && (m > 96 || n <= 16384) &&
+    (void)n;
+    return m > MMQS_MAX_ROWS &&
            (type == Q4_K || type == Q4_0 || type == Q8_0 || type == IQ3_S || type == Q2_K);
 }
 void launch_mmq_h(int type, const void *weight, int64_t n, int64_t k, int64_t m, const MmqhImage &image,

@@ -127,22 +127,22 @@ H_TYPES = (O.Q4_K, O.Q4_0, O.Q8_0, O.IQ3_S, O.Q2_K)  # the fp16 GEMM's formats (
 
 
 def _uses_h(qtype, m, n):
-    """The batched route rule: the fp16 GEMM above 16 rows for its formats, except that up to
-    96 rows a matrix of more than 16384 rows stays on the int8 tile kernel."""
-    return qtype in H_TYPES and m > 16 and (m > 96 or n <= 16384)
+    """The batched route rule: the fp16 GEMM above 16 rows for its formats."""
+    return qtype in H_TYPES and m > 16
 
 
 def test_mmq_workspace_follows_the_route_rule(kai):
-    """A 34816-row Q4_K matrix at 80 rows reads the int8 DS4 plane; at 5120 rows, or at 97
-    rows, the fp16 image."""
+    """Above 16 rows Q4_K reads the fp16 image (34816 or 5120 rows, 80 or 97 rows); Q6_K, on
+    the int8 tile kernel, reads its plane (the D2S6 plane has the DS4 plane's size)."""
     a256 = lambda b: (b + 255) // 256 * 256
-    types = (ctypes.c_int * 1)(O.Q4_K)
-    for n, m, image in ((34816, 80, False), (5120, 80, True), (34816, 97, True)):
+    for qtype, n, m, image in ((O.Q4_K, 34816, 80, True), (O.Q4_K, 5120, 80, True), (O.Q4_K, 34816, 97, True),
+                               (O.Q6_K, 5120, 80, False)):
+        types = (ctypes.c_int * 1)(qtype)
         rows = (ctypes.c_int64 * 1)(n)
         got = kai.kai_fused_mmq_workspace(0, types, rows, 1, 5120, m, 1)
         base = a256(4 * m) + (_h_image_bytes(O.DS4, m, 5120) if image else a256(_plane_bytes(m, 5120)))
         assert base <= got, (n, m)
-        assert _uses_h(O.Q4_K, m, n) == image
+        assert _uses_h(qtype, m, n) == image
         # the remainder is the fp16 GEMM's split-K sums (at most 8 splits of m x n fp32); the int8
         # tile kernel has none
         assert (got - base) % 256 == 0 and got - base <= a256(8 * m * n * 4), (n, m, got - base)
