@@ -42,8 +42,9 @@
 //   producers: copy stage s + 1's activation chunks from global memory straight into LDS
 //     (global_load_lds_dwordx4, no registers) and wait for them at the stage's end; at a step's
 //     first stage, write step i + 1's wire bytes (loaded a step earlier) to raw LDS and load
-//     step i + 2's; convert stage s + 1's weights from raw LDS when s + 1 is even; at a step's
-//     third stage, the next superblock's min-pass factors (WMIN);
+//     step i + 2's (Q4_K, whose step is nine whole 16-byte copies: copy step i + 1's wire bytes
+//     straight into raw LDS instead); convert stage s + 1's weights from raw LDS when s + 1 is
+//     even; at a step's third stage, the next superblock's min-pass factors (WMIN);
 //   compute: stage s's MFMAs from LDS stage s % 2, at a step's first stage also the min pass;
 //     then convert stage s + 1's weights when s + 1 is odd.
 // The barrier is a bare s_barrier after lgkmcnt(0) (a memory fence would wait for every load in
@@ -401,10 +402,33 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
             for (int p = 0; p < RPT; ++p)
                 if (RAWC % THREADS == 0 || ptid + p * THREADS < RAWC) store_unaligned(rb + raw_at[p] + raw_off[p], rawv[p]);
         };
+        // RAW_DMA (whole 256-value steps whose wire bytes are a whole number of 16-byte copies:
+        // Q4_K): copy c of a step lands at 16 c of the raw step, so a wave's copies fill 1 KiB in
+        // lane order and go straight from global memory to LDS, as the activation does (below).
+        // The last copy index may end inside the waves; RAWC is a whole number of waves, so a wave
+        // issues all of a copy index or none of it.
+        constexpr bool RAW_DMA = !SHORT && W::SEG == W::RS && W::SEG % 16 == 0;
+        static_assert(!RAW_DMA || RAWC % WAVE == 0, "whole waves of wire-byte copies");
+        const int pwave = __builtin_amdgcn_readfirstlane(ptid / WAVE);
+        const bool raw_all = RAWC % THREADS == 0 || (RPT - 1) * THREADS + WAVE * pwave < RAWC;  // uniform
+        auto rdma = [&](int step, lds_u8 *rb) __attribute__((always_inline)) {
+#pragma unroll
+            for (int p = 0; p < RPT; ++p) {
+                if (p < RPT - 1 || raw_all) {
+                    const uint32_t la = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(rb + 16 * (p * THREADS + WAVE * pwave)));
+                    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                                 :: "s"(la), "v"(raw_row[p] + int64_t(step) * W::SEG + raw_piece[p]) : "memory", "m0");
+                }
+            }
+        };
+        // all but the wire-byte copies just issued are done (their count is the wave's)
+        auto wait_but_raw = [&]() __attribute__((always_inline)) {
+            if (raw_all) mmqh_wait_loads<RPT>();
+            else mmqh_wait_loads<RPT - 1>();
+        };
         // activation: per stage, the image's 16-byte chunks (4 groups x BM rows x 32 bytes; chunk
-        // w of a group holds row w / 2, half (w % 2) swizzled), loaded two stages ahead (ring of
-        // 4 in registers) and written to LDS a stage ahead; per superblock its min-pass operands
-        // (BM x AB bytes). Rows past the image read its last row.
+        // w of a group holds row w / 2, half (w % 2) swizzled), copied to LDS a stage ahead; per
+        // superblock its min-pass operands (BM x AB bytes). Rows past the image read its last row.
         const int rows_here = min(BM, img.mpad - m0);
         constexpr int MIN_CH = AB * BM / 16;
         constexpr int CODE_PW = 8 * BM / THREADS, MIN_PW = (MIN_CH + THREADS - 1) / THREADS;
@@ -424,7 +448,6 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
         // else in the kernel uses M0. The compiler does not count these loads, so its own waits
         // for the loads issued before them wait longer, never shorter; the stage's waits for
         // the copies are explicit (mmqh_wait_loads).
-        const int pwave = __builtin_amdgcn_readfirstlane(ptid / WAVE);
         auto adma = [&](int s, lds_u8 *ab) __attribute__((always_inline)) {
             const uint8_t *cb = img.codes + (int64_t(4 * s) * img.mpad + m0) * 32;
 #pragma unroll
@@ -455,12 +478,13 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
             constexpr int J = decltype(jtag)::value;
             const int sw = min(s + 1, last), step = s >> 2;
             // the register stores first: their waits then cover only the copies of earlier stages
-            if constexpr (J == 0) rstore(raw_of(step + 1));
+            if constexpr (!RAW_DMA && J == 0) rstore(raw_of(step + 1));
             if constexpr (MIN_PW > 0 && J == 3) mstore();
             __builtin_amdgcn_sched_barrier(0);
             adma(sw, anext);
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (J == 0) rload(min(step + 2, last >> 2));
+            if constexpr (!RAW_DMA && J == 0) rload(min(step + 2, last >> 2));
+            if constexpr (RAW_DMA && J == 0) rdma(min(step + 1, last >> 2), raw_of(step + 1));
             if constexpr (MIN_PW > 0 && J == 1) mload(min(s + 3, last) / 4 * 4);
             // the next superblock's min-pass factors a stage before its first conversion (the
             // compute waves read WMIN at each superblock's first stage only)
@@ -468,20 +492,30 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
             if constexpr (J == 1 || J == 3) wstore(sw, wnext, std::false_type{});
             (void)wnext;
             __builtin_amdgcn_sched_barrier(0);
-            mmqh_wait_loads<(J == 0 ? RPT : 0) + (J == 1 ? MIN_PW : 0)>();
+            if constexpr (J == 0 && RAW_DMA) wait_but_raw();
+            else mmqh_wait_loads<(J == 0 ? RPT : 0) + (J == 1 ? MIN_PW : 0)>();
             mmqh_barrier();
         };
         if constexpr (TYPE == IQ3_S) mmqh_barrier();  // the grid, before the first conversion
         if (s0 < s1) {
-            rload(s0 >> 2);
-            rstore(raw_of(s0 >> 2));
-            if constexpr (MIN_PW > 0) mload(s0);
-            adma(s0, A0);
-            __builtin_amdgcn_sched_barrier(0);
-            rload(min((s0 >> 2) + 1, last >> 2));
-            if constexpr (MIN_PW > 0) mstore();
-            __builtin_amdgcn_sched_barrier(0);
-            mmqh_wait_loads<RPT>();
+            if constexpr (RAW_DMA) {
+                rdma(s0 >> 2, raw_of(s0 >> 2));
+                if constexpr (MIN_PW > 0) mload(s0);
+                adma(s0, A0);
+                if constexpr (MIN_PW > 0) mstore();
+                __builtin_amdgcn_sched_barrier(0);
+                mmqh_wait_loads<0>();
+            } else {
+                rload(s0 >> 2);
+                rstore(raw_of(s0 >> 2));
+                if constexpr (MIN_PW > 0) mload(s0);
+                adma(s0, A0);
+                __builtin_amdgcn_sched_barrier(0);
+                rload(min((s0 >> 2) + 1, last >> 2));
+                if constexpr (MIN_PW > 0) mstore();
+                __builtin_amdgcn_sched_barrier(0);
+                mmqh_wait_loads<RPT>();
+            }
             mmqh_barrier();  // the wire bytes of the first step, its activation and min operands
             wstore(s0, W0, std::true_type{});
             mmqh_barrier();
