@@ -471,9 +471,11 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
         // stage J of a step i (s = 4 i + J): copy stage s + 1's activation into LDS first; the
         // min-pass operands of a superblock are loaded two stages before its first stage (J = 1)
         // and written a stage before it (J = 3); at J = 0 the wire bytes of step i + 1 (loaded
-        // at step i - 1) go to raw LDS and those of step i + 2 are loaded. Loads complete in
-        // issue order for the wait counter, so the wait for the stage's copies before the
-        // barrier leaves the loads issued after them in flight.
+        // at step i - 1) go to raw LDS and those of step i + 2 are loaded (RAW_DMA: step i + 1's
+        // are copied into its raw buffer, whose last reader, the conversion of step i - 1's last
+        // stage, ran two stages before; their first reader, the min-pass factors at J = 2, comes
+        // after J = 1's wait). Loads complete in issue order for the wait counter, so the wait
+        // for the stage's copies before the barrier leaves the loads issued after them in flight.
         auto pstep = [&](int s, auto jtag, lds_u8 *anext, lds_u8 *wnext) __attribute__((always_inline)) {
             constexpr int J = decltype(jtag)::value;
             const int sw = min(s + 1, last), step = s >> 2;
