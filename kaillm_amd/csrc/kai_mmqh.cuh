@@ -56,9 +56,11 @@
 // were part of every stage.
 // Rows past the activation image and past the matrix are clamped; their outputs are never
 // stored. Split-K (grid.y > 1): each split writes its fp32 sums to scratch and
-// mmqh_reduce_kernel adds them in split order.
+// mmqh_reduce_kernel adds them in split order; the same for the K pieces of a tail's tiles
+// (MmqhTail), over the tail's rectangle of the output.
 #pragma once
 
+#include <algorithm>
 #include <type_traits>
 
 #include "kai_mmq_formats.h"
@@ -73,6 +75,14 @@ typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 struct MmqhArgs {
     const uint8_t *codes, *mins;
     int mpad;
+};
+// A launch whose last round of workgroups would be a small fraction of the CUs: the first
+// `main` tiles run whole (K unsplit), the rest, all inside the last activation tile (its rows
+// [r0, r0 + rows), weight rows [c0, c0 + cols)), run in `splits` K pieces of `stages` stages
+// whose fp32 sums go to scratch [piece][rows][cols] for mmqh_reduce_kernel. No tail: main is
+// every tile.
+struct MmqhTail {
+    int main, splits, stages, r0, rows, c0, cols;
 };
 
 __device__ __forceinline__ uint32_t h2_bits(h2_t v) { return __builtin_bit_cast(uint32_t, v); }
@@ -282,7 +292,7 @@ template <int TYPE, int WN, int WM, int GN, int GM>
 __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2, 2))) void mmqh_kernel(
     const uint8_t *__restrict__ weight, int64_t row_bytes, int n, int k, MmqhArgs img, int m,
     const float *__restrict__ inverse, void *__restrict__ dst, int64_t stride_dst, int dst_bf16,
-    float *__restrict__ partial, int tiles_n, int tiles_m, int split_stages) {
+    float *__restrict__ partial, int tiles_n, int tiles_m, int split_stages, MmqhTail tail) {
     using W = MmqhW<TYPE>;
     constexpr int CW = GN * GM, THREADS = 64 * CW, BN = 32 * WN * GN, BM = 32 * WM * GM;
     constexpr int AB = mmqh_amin_bytes<TYPE>();
@@ -307,16 +317,23 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
 
     const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
     // tile of this workgroup: each XCD (workgroups dealt round-robin over 8) gets a contiguous
-    // range of tiles, weight tiles fastest, so the workgroups running together on an XCD share
-    // an activation tile in its L2
-    const int tiles = tiles_n * tiles_m;
-    int t = blockIdx.x;
-    if (tiles % 8 == 0) t = (t % 8) * (tiles / 8) + t / 8;
+    // range of the whole tiles, weight tiles fastest, so the workgroups running together on an
+    // XCD share an activation tile in its L2; a tail workgroup takes one K piece of a tail tile
+    int t = blockIdx.x, piece = blockIdx.y, piece_stages = split_stages;
+    const bool tail_piece = t >= tail.main;  // uniform
+    if (tail_piece) {
+        const int q = t - tail.main;
+        t = tail.main + q / tail.splits;
+        piece = q % tail.splits;
+        piece_stages = tail.stages;
+    } else if (tail.main % 8 == 0) {
+        t = (t % 8) * (tail.main / 8) + t / 8;
+    }
     const int n0 = (t % tiles_n) * BN, m0 = (t / tiles_n) * BM;
-    // K runs to the image's padding, whole steps of 256 values; split_stages is a multiple of 4,
-    // so every split is whole steps and s % 4 is the stage's place in its step
+    // K runs to the image's padding, whole steps of 256 values; the pieces are multiples of 4
+    // stages, so every piece is whole steps and s % 4 is the stage's place in its step
     const int stages = (k + 255) / 256 * 4;
-    const int s0 = blockIdx.y * split_stages, s1 = min(stages, s0 + split_stages), last = s1 - 1;
+    const int s0 = piece * piece_stages, s1 = min(stages, s0 + piece_stages), last = s1 - 1;
     if constexpr (TYPE == IQ3_S) {
         for (int i = tid; i < 512; i += 2 * THREADS) grid_lds[i] = mmq_iq3s_grid[i];
     }
@@ -614,14 +631,18 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
     // element stores (Q4_K 34816 x 5120 at 2048 rows 1235 -> 1063 us, 5120 x 17408 818 -> 655 us).
     auto store_all = [&](auto kind_tag) __attribute__((always_inline)) {
         constexpr int KIND = decltype(kind_tag)::value;  // 0 partial sums, 1 f32, 2 bf16
-        const bool vec = KIND == 0 ? n % 4 == 0
+        // partial sums: [split][m][n], or a tail piece's [piece][tail rows][tail cols]
+        const int64_t pstride = tail_piece ? tail.cols : n;
+        float *const pbase = tail_piece ? partial + (int64_t(piece) * tail.rows - tail.r0) * pstride - tail.c0
+                                        : partial + int64_t(piece) * m * n;
+        const bool vec = KIND == 0 ? pstride % 4 == 0
                                    : stride_dst % 4 == 0 && (reinterpret_cast<uintptr_t>(dst) & (KIND == 1 ? 15 : 7)) == 0;
 #pragma unroll
         for (int tm = 0; tm < WM; ++tm) {
             const int i = m0 + arow0 + 32 * tm + col;
             if (i >= m) continue;
             const float inv = KIND == 0 ? 1.0f : inverse[i];
-            float *rowf = KIND == 0 ? partial + (int64_t(blockIdx.y) * m + i) * n
+            float *rowf = KIND == 0 ? pbase + int64_t(i) * pstride
                                     : static_cast<float *>(dst) + int64_t(i) * stride_dst;
             uint16_t *rowh = static_cast<uint16_t *>(dst) + int64_t(i) * stride_dst;
 #pragma unroll
@@ -652,7 +673,7 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
             }
         }
     };
-    if (partial) store_all(std::integral_constant<int, 0>{});
+    if (tail_piece || gridDim.y > 1) store_all(std::integral_constant<int, 0>{});
     else if (dst_bf16) store_all(std::integral_constant<int, 2>{});
     else store_all(std::integral_constant<int, 1>{});
 }
@@ -674,7 +695,12 @@ struct MmqhConfig {
 struct MmqhPlan {
     MmqhConfig cfg;
     int tiles_n = 0, tiles_m = 0, splits = 1, split_stages = 0;
+    MmqhTail tail = {};
+    bool has_tail() const { return tail.main < tiles_n * tiles_m; }
 };
+// Scratch a tail's K pieces may use: written once and read once, 32 MiB cost ~13 us at HBM
+// rate, against the tens of microseconds of a last round cut to an eighth or a half.
+constexpr size_t MMQH_TAIL_BYTES = size_t(32) << 20;
 constexpr int MMQH_CUS = 256;
 template <int TYPE, int WN, int WM, int GN, int GM>
 constexpr bool mmqh_fits() {
@@ -714,6 +740,30 @@ inline void mmqh_consider(MmqhPlan &best, double &best_t, int64_t n, int64_t k, 
         }
     }
 }
+// An unsplit plan whose last round of workgroups would hold at most half the CUs' worth of
+// tiles: those tiles (the last ones, inside the last activation tile) run in K pieces instead,
+// as many as fill the round's CUs, at most 8 and at most MMQH_TAIL_BYTES of sums. Measured on
+// MI355X, Q4_K 34816 x 5120: at 512 rows (544 tiles of 256 x 128, a third round of 32, now 8
+// pieces) 303 -> 251 us; at 2048 rows (a ninth round of 128, now 2 pieces) 922 -> 915 us
+// (a half-empty round already runs faster per tile); IQ3_S at 2048 rows 1048 -> 1018 us.
+inline void mmqh_tail(MmqhPlan &p, int64_t n, int64_t k, int64_t m) {
+    const int tiles = p.tiles_n * p.tiles_m, slots = MMQH_CUS;
+    p.tail = {tiles, 1, 0, 0, 0, 0, 0};
+    if (p.splits != 1) return;
+    const int rem = tiles % slots, full = tiles - rem;
+    if (full == 0 || rem == 0 || 2 * rem > slots || rem > p.tiles_n) return;
+    const int64_t r0 = int64_t(p.tiles_m - 1) * p.cfg.bm(), c0 = int64_t(p.tiles_n - rem) * p.cfg.bn();
+    const int64_t rows = std::min<int64_t>(p.cfg.bm(), m - r0), cols = n - c0;
+    const int stages = static_cast<int>((k + 255) / 256 * 4);
+    int64_t pieces = std::min<int64_t>({slots / rem, 8, stages / 4,
+                                        static_cast<int64_t>(MMQH_TAIL_BYTES / size_t(rows * cols * 4))});
+    if (pieces < 2) return;
+    const int chunk = static_cast<int>(((stages + pieces - 1) / pieces + 3) / 4 * 4);
+    pieces = (stages + chunk - 1) / chunk;
+    if (pieces < 2) return;
+    p.tail = {full, static_cast<int>(pieces), chunk, static_cast<int>(r0), static_cast<int>(rows), static_cast<int>(c0),
+              static_cast<int>(cols)};
+}
 template <int TYPE>
 inline MmqhPlan mmqh_plan(int64_t n, int64_t k, int64_t m) {
     MmqhPlan best;
@@ -728,10 +778,13 @@ inline MmqhPlan mmqh_plan(int64_t n, int64_t k, int64_t m) {
             mmqh_consider<TYPE, 2, 2, 2, 2>(best, t, n, k, m);
         }
     }
+    mmqh_tail(best, n, k, m);
     return best;
 }
 inline size_t mmqh_partial_bytes(const MmqhPlan &p, int64_t m, int64_t n) {
-    return p.splits > 1 ? size_t(p.splits) * size_t(m) * size_t(n) * sizeof(float) : 0;
+    if (p.splits > 1) return size_t(p.splits) * size_t(m) * size_t(n) * sizeof(float);
+    if (p.has_tail()) return size_t(p.tail.splits) * size_t(p.tail.rows) * size_t(p.tail.cols) * sizeof(float);
+    return 0;
 }
 
 template <int TYPE, int WN, int WM, int GN, int GM>
@@ -741,14 +794,24 @@ void launch_mmqh_cfg(const void *weight, int64_t n, int64_t k, int64_t m, const 
     constexpr int BN = 32 * WN * GN, BM = 32 * WM * GM;
     static_assert(MmqhLds<TYPE, BN, BM>::TOTAL <= 160 * 1024, "mmqh LDS");  // static arrays
     const int64_t row_bytes = (k / block_elems(TYPE)) * block_bytes(TYPE);
-    const dim3 grid(static_cast<unsigned>(p.tiles_n * p.tiles_m), static_cast<unsigned>(p.splits));
+    const int tiles = p.tiles_n * p.tiles_m;
+    const int wgs = p.has_tail() ? p.tail.main + (tiles - p.tail.main) * p.tail.splits : tiles;
+    const dim3 grid(static_cast<unsigned>(wgs), static_cast<unsigned>(p.splits));
     mmqh_kernel<TYPE, WN, WM, GN, GM><<<grid, 128 * GN * GM, 0, stream>>>(
         static_cast<const uint8_t *>(weight), row_bytes, static_cast<int>(n), static_cast<int>(k), img,
-        static_cast<int>(m), inverse, dst, stride_dst, dst_bf16 ? 1 : 0, p.splits > 1 ? partial : nullptr, p.tiles_n,
-        p.tiles_m, p.split_stages);
-    if (p.splits > 1)
+        static_cast<int>(m), inverse, dst, stride_dst, dst_bf16 ? 1 : 0, partial, p.tiles_n, p.tiles_m,
+        p.split_stages, p.tail);
+    if (p.splits > 1) {
         mmqh_reduce_kernel<<<static_cast<unsigned>((m * n + 1023) / 1024), 256, 0, stream>>>(
             partial, p.splits, static_cast<int>(m), static_cast<int>(n), inverse, dst, stride_dst, dst_bf16 ? 1 : 0);
+    } else if (p.has_tail()) {  // the tail tiles' rectangle of the output
+        const MmqhTail &t = p.tail;
+        const int64_t at = int64_t(t.r0) * stride_dst + t.c0;
+        void *tail_dst = dst_bf16 ? static_cast<void *>(static_cast<uint16_t *>(dst) + at)
+                                  : static_cast<void *>(static_cast<float *>(dst) + at);
+        mmqh_reduce_kernel<<<static_cast<unsigned>((int64_t(t.rows) * t.cols + 1023) / 1024), 256, 0, stream>>>(
+            partial, t.splits, t.rows, t.cols, inverse + t.r0, tail_dst, stride_dst, dst_bf16 ? 1 : 0);
+    }
 }
 
 template <int TYPE>
@@ -757,7 +820,7 @@ void launch_mmqh(const void *weight, int64_t n, int64_t k, int64_t m, const Mmqh
                  hipStream_t stream) {
     static_assert(mmqh_type<TYPE>(), "fp16 GEMM format");
     const MmqhPlan p = mmqh_plan<TYPE>(n, k, m);
-    if (mmqh_partial_bytes(p, m, n) > partial_bytes || (p.splits > 1 && !partial))
+    if (mmqh_partial_bytes(p, m, n) > partial_bytes || ((p.splits > 1 || p.has_tail()) && !partial))
         throw Error("Scratch too small for the fp16 GEMM's split-K sums");
     if (n * ((k / block_elems(TYPE)) * block_bytes(TYPE)) >= (int64_t(1) << 40)) throw Error("Matrix too large");
     // the short formats' wire-byte copies are 16 bytes, within the row's last step: one block at least

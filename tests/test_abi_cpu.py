@@ -150,6 +150,22 @@ def test_mmq_workspace_follows_the_route_rule(kai):
             assert got == base, (n, m, got - base)
 
 
+def test_mmq_workspace_holds_the_tail_pieces(kai):
+    """More fp16 GEMM tiles than CUs with at most half the CUs' worth left for the last round:
+    those last tiles (inside the last activation tile) run in K pieces (at most 8, whole
+    256-value steps, as many as the idle CUs take), whose sums are pieces x rows x columns
+    fp32. Q4_K 18000 x 1024 at 300 rows: 2 x 141 tiles of 256 x 128, the last 26 in 4 pieces
+    over rows 256..299 and columns 14720..17999; Q2_K 11000 x 2048 at 260 rows: 3 x 86 tiles of
+    128 x 128, the last 2 in 8 pieces over rows 256..259 and columns 10752..10999."""
+    a256 = lambda b: (b + 255) // 256 * 256
+    for qtype, n, k, m, pieces in ((O.Q4_K, 18000, 1024, 300, 4 * 44 * 3280), (O.Q2_K, 11000, 2048, 260, 8 * 4 * 248)):
+        types = (ctypes.c_int * 1)(qtype)
+        rows = (ctypes.c_int64 * 1)(n)
+        got = kai.kai_fused_mmq_workspace(0, types, rows, 1, k, m, 1)
+        base = a256(4 * m) + _h_image_bytes(O.mmq_layout(qtype), m, k)
+        assert got - base == a256(4 * pieces), (O.NAMES[qtype], got - base)
+
+
 def _h_image_bytes(layout, m, k):
     """The fp16 GEMM's image of one layout: codes and min-pass sums, each 256-aligned."""
     a256 = lambda b: (b + 255) // 256 * 256
