@@ -740,16 +740,19 @@ inline void mmqh_consider(MmqhPlan &best, double &best_t, int64_t n, int64_t k, 
         }
     }
 }
-// An unsplit plan whose last round of workgroups would hold at most half the CUs' worth of
-// tiles: those tiles (the last ones, inside the last activation tile) run in K pieces instead,
-// as many as fill the round's CUs, at most 8 and at most MMQH_TAIL_BYTES of sums. Measured on
-// MI355X, Q4_K 34816 x 5120: at 512 rows (544 tiles of 256 x 128, a third round of 32, now 8
-// pieces) 303 -> 251 us; at 2048 rows (a ninth round of 128, now 2 pieces) 922 -> 915 us
-// (a half-empty round already runs faster per tile); IQ3_S at 2048 rows 1048 -> 1018 us.
-inline void mmqh_tail(MmqhPlan &p, int64_t n, int64_t k, int64_t m) {
+// A plan with more tiles than CUs whose last round of workgroups would hold at most half the
+// CUs' worth of tiles: the last tiles (inside the last activation tile) run in K pieces, as
+// many as fill that round's CUs, at most 8 and at most MMQH_TAIL_BYTES of sums, the others
+// whole. Taken where the cost model of mmqh_consider puts it ahead of the chosen plan (an
+// unsplit one's last round, or a K split's extra rounds). Measured on MI355X, Q4_K
+// 34816 x 5120: at 512 rows (544 tiles of 256 x 128, a third round of 32, now 7 pieces)
+// 303 -> 251 us; at 2048 rows (a ninth round of 128, now 2 pieces) 922 -> 915 us (a half-empty
+// round already runs faster per tile); IQ3_S at 2048 rows 1048 -> 1018 us; in place of a
+// three-way K split (272 tiles: 256 whole, 16 in 7 pieces) at 17 / 80 / 97 / 256 rows
+// 95 / 103 / 112 / 185 -> 81 / 80 / 92 / 144 us.
+inline void mmqh_tail(MmqhPlan &p, double best_t, int64_t n, int64_t k, int64_t m) {
     const int tiles = p.tiles_n * p.tiles_m, slots = MMQH_CUS;
     p.tail = {tiles, 1, 0, 0, 0, 0, 0};
-    if (p.splits != 1) return;
     const int rem = tiles % slots, full = tiles - rem;
     if (full == 0 || rem == 0 || 2 * rem > slots || rem > p.tiles_n) return;
     const int64_t r0 = int64_t(p.tiles_m - 1) * p.cfg.bm(), c0 = int64_t(p.tiles_n - rem) * p.cfg.bn();
@@ -761,6 +764,13 @@ inline void mmqh_tail(MmqhPlan &p, int64_t n, int64_t k, int64_t m) {
     const int chunk = static_cast<int>(((stages + pieces - 1) / pieces + 3) / 4 * 4);
     pieces = (stages + chunk - 1) / chunk;
     if (pieces < 2) return;
+    // mmqh_consider's units: whole rounds of whole tiles, the pieces' round, their sums
+    const double tile_time = double(p.cfg.wn * p.cfg.gn * p.cfg.wm * p.cfg.gm);
+    const double t = double(full / slots) * tile_time + tile_time * chunk / stages +
+                     double(pieces) * double(rows) * double(cols) / (320.0 * double(k));
+    if (t >= best_t) return;
+    p.splits = 1;
+    p.split_stages = stages;
     p.tail = {full, static_cast<int>(pieces), chunk, static_cast<int>(r0), static_cast<int>(rows), static_cast<int>(c0),
               static_cast<int>(cols)};
 }
@@ -778,7 +788,7 @@ inline MmqhPlan mmqh_plan(int64_t n, int64_t k, int64_t m) {
             mmqh_consider<TYPE, 2, 2, 2, 2>(best, t, n, k, m);
         }
     }
-    mmqh_tail(best, n, k, m);
+    mmqh_tail(best, t, n, k, m);
     return best;
 }
 inline size_t mmqh_partial_bytes(const MmqhPlan &p, int64_t m, int64_t n) {

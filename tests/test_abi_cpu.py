@@ -156,9 +156,12 @@ def test_mmq_workspace_holds_the_tail_pieces(kai):
     256-value steps, as many as the idle CUs take), whose sums are pieces x rows x columns
     fp32. Q4_K 18000 x 1024 at 300 rows: 2 x 141 tiles of 256 x 128, the last 26 in 4 pieces
     over rows 256..299 and columns 14720..17999; Q2_K 11000 x 2048 at 260 rows: 3 x 86 tiles of
-    128 x 128, the last 2 in 8 pieces over rows 256..259 and columns 10752..10999."""
+    128 x 128, the last 2 in 8 pieces over rows 256..259 and columns 10752..10999; in place of a
+    K split, Q4_0 and IQ3_S 33000 x 1024 at 40 and 120 rows: 258 tiles of 128 weight rows, the
+    last 2 in 4 pieces over every row and columns 32768..32999."""
     a256 = lambda b: (b + 255) // 256 * 256
-    for qtype, n, k, m, pieces in ((O.Q4_K, 18000, 1024, 300, 4 * 44 * 3280), (O.Q2_K, 11000, 2048, 260, 8 * 4 * 248)):
+    for qtype, n, k, m, pieces in ((O.Q4_K, 18000, 1024, 300, 4 * 44 * 3280), (O.Q2_K, 11000, 2048, 260, 8 * 4 * 248),
+                                   (O.Q4_0, 33000, 1024, 40, 4 * 40 * 232), (O.IQ3_S, 33000, 1024, 120, 4 * 120 * 232)):
         types = (ctypes.c_int * 1)(qtype)
         rows = (ctypes.c_int64 * 1)(n)
         got = kai.kai_fused_mmq_workspace(0, types, rows, 1, k, m, 1)

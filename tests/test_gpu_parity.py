@@ -532,15 +532,19 @@ def test_batched_prefill_tiles(kai, qtype, weights, m, n, k):
 
 
 # More tiles than CUs with a short last round: the last tiles (inside the last activation tile)
-# run in K pieces whose sums a second kernel adds into that rectangle of the output. Q4_K on
-# 256 x 128 tiles: 2 x 141 tiles, the last 26 in 4 pieces of one 256-value step, the rectangle
-# 44 rows by 3280 columns (the last tile 80 wide); Q2_K on 128 x 128 tiles: 3 x 86 tiles, the
-# last 2 in 8 pieces, the rectangle 4 rows by 248 columns.
-TAIL = [(O.Q4_K, 300, 18000, 1024), (O.Q2_K, 260, 11000, 2048)]
+# run in K pieces whose sums a second kernel adds into that rectangle of the output, in place of
+# an unsplit plan's short round or a K split's extra rounds. Q4_K on 256 x 128 tiles: 2 x 141
+# tiles, the last 26 in 4 pieces of one 256-value step, the rectangle rows 256..299 by 3280
+# columns (the last tile 80 wide); Q2_K on 128 x 128 tiles: 3 x 86 tiles, the last 2 in 8
+# pieces, the rectangle 4 rows by 248 columns; Q4_0 at 40 rows on 128 x 96 tiles and IQ3_S at
+# 120 rows on 128 x 128 tiles: 258 tiles, the last 2 (232 columns, the last tile 104 wide) in 4
+# pieces over every row.
+TAIL = [(O.Q4_K, 300, 18000, 1024, 256), (O.Q2_K, 260, 11000, 2048, 256), (O.Q4_0, 40, 33000, 1024, 0),
+        (O.IQ3_S, 120, 33000, 1024, 0)]
 
 
-@pytest.mark.parametrize("qtype,m,n,k", TAIL, ids=[f"{O.NAMES[t]}-{m}x{n}x{k}" for t, m, n, k in TAIL])
-def test_batched_tail_tiles_in_k_pieces(kai, qtype, m, n, k):
+@pytest.mark.parametrize("qtype,m,n,k,r0", TAIL, ids=[f"{O.NAMES[t]}-{m}x{n}x{k}" for t, m, n, k, _ in TAIL])
+def test_batched_tail_tiles_in_k_pieces(kai, qtype, m, n, k, r0):
     print(f"batched tail tiles {O.NAMES[qtype]} m={m} n={n} k={k}", flush=True)
     rng = np.random.default_rng(qtype + m)
     w = O.random_blocks(qtype, n, k, rng)
@@ -548,14 +552,15 @@ def test_batched_tail_tiles_in_k_pieces(kai, qtype, m, n, k):
     ref = O.mmq_reference(qtype, w, x, threads=16)
     mats = [(qtype, w, to_dev(w))]
     out = gpu_mmq(kai, mats, to_dev(x)).cpu().numpy()
-    r0 = 256  # the last activation tile's first row on either tile height
+    c0 = n - 232 if r0 == 0 else 0
     assert O.normwise_rel(out, ref) <= TOL_F32
-    assert O.normwise_rel(out[r0:], ref[r0:]) <= TOL_F32
+    assert O.normwise_rel(out[r0:, c0:], ref[r0:, c0:]) <= TOL_F32
     again = gpu_mmq(kai, mats, to_dev(x)).cpu().numpy()
     assert np.array_equal(out, again), "the pieces are added in a fixed order"
     outb = gpu_mmq(kai, mats, to_dev(x), bf16=True, stride=n + 3).float().cpu().numpy()
     assert O.normwise_rel(outb[:, :n], ref) <= TOL_BF16
-    assert O.normwise_rel(outb[r0:, :n], ref[r0:]) <= TOL_BF16
+    # the same sums as the f32 output, rounded to nearest even once (pieces and whole tiles)
+    assert np.array_equal(outb[:, :n], torch.from_numpy(out).to(torch.bfloat16).float().numpy())
     assert np.isnan(outb[:, n:]).all()
 
 
