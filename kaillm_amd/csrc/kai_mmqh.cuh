@@ -76,11 +76,11 @@ struct MmqhArgs {
     const uint8_t *codes, *mins;
     int mpad;
 };
-// A launch whose last round of workgroups would be a small fraction of the CUs: the first
-// `main` tiles run whole (K unsplit), the rest, all inside the last activation tile (its rows
-// [r0, r0 + rows), weight rows [c0, c0 + cols)), run in `splits` K pieces of `stages` stages
-// whose fp32 sums go to scratch [piece][rows][cols] for mmqh_reduce_kernel. No tail: main is
-// every tile.
+// A launch whose last round of workgroups would be a small fraction of the CUs: the tiles of a
+// rectangle at the output's end (activation rows [r0, r0 + rows) = [r0, m), weight rows
+// [c0, c0 + cols) = [c0, n), r0 and c0 on tile bounds) run in `splits` K pieces of `stages`
+// stages whose fp32 sums go to scratch [piece][rows][cols] for mmqh_reduce_kernel; the other
+// `main` tiles run whole (K unsplit). No tail: main is every tile and rows is 0.
 struct MmqhTail {
     int main, splits, stages, r0, rows, c0, cols;
 };
@@ -318,18 +318,30 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
     const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
     // tile of this workgroup: each XCD (workgroups dealt round-robin over 8) gets a contiguous
     // range of the whole tiles, weight tiles fastest, so the workgroups running together on an
-    // XCD share an activation tile in its L2; a tail workgroup takes one K piece of a tail tile
-    int t = blockIdx.x, piece = blockIdx.y, piece_stages = split_stages;
+    // XCD share an activation tile in its L2. The whole tiles are those of the activation tiles
+    // above the tail's rectangle, then those left of it; a tail workgroup takes one K piece of
+    // a tile of the rectangle.
+    int t = blockIdx.x, piece = blockIdx.y, piece_stages = split_stages, tile_m, tile_n;
     const bool tail_piece = t >= tail.main;  // uniform
+    const int tr0 = tail.r0 / BM, tc0 = tail.c0 / BN;
     if (tail_piece) {
-        const int q = t - tail.main;
-        t = tail.main + q / tail.splits;
+        const int q = t - tail.main, tt = q / tail.splits, width = tiles_n - tc0;
+        tile_m = tr0 + tt / width;
+        tile_n = tc0 + tt % width;
         piece = q % tail.splits;
         piece_stages = tail.stages;
-    } else if (tail.main % 8 == 0) {
-        t = (t % 8) * (tail.main / 8) + t / 8;
+    } else {
+        if (tail.main % 8 == 0) t = (t % 8) * (tail.main / 8) + t / 8;
+        if (tail.rows > 0 && t >= tr0 * tiles_n) {  // beside the rectangle: tc0 > 0
+            const int u = t - tr0 * tiles_n;
+            tile_m = tr0 + u / tc0;
+            tile_n = u % tc0;
+        } else {
+            tile_m = t / tiles_n;
+            tile_n = t % tiles_n;
+        }
     }
-    const int n0 = (t % tiles_n) * BN, m0 = (t / tiles_n) * BM;
+    const int n0 = tile_n * BN, m0 = tile_m * BM;
     // K runs to the image's padding, whole steps of 256 values; the pieces are multiples of 4
     // stages, so every piece is whole steps and s % 4 is the stage's place in its step
     const int stages = (k + 255) / 256 * 4;
@@ -749,14 +761,20 @@ inline void mmqh_consider(MmqhPlan &best, double &best_t, int64_t n, int64_t k, 
 // 303 -> 251 us; at 2048 rows (a ninth round of 128, now 2 pieces) 922 -> 915 us (a half-empty
 // round already runs faster per tile); IQ3_S at 2048 rows 1048 -> 1018 us; in place of a
 // three-way K split (272 tiles: 256 whole, 16 in 7 pieces) at 17 / 80 / 97 / 256 rows
-// 95 / 103 / 112 / 185 -> 81 / 80 / 92 / 144 us.
+// 95 / 103 / 112 / 185 -> 81 / 80 / 92 / 144 us; Q4_K 5120 x 17408 at 2048 rows, in place of a
+// four-way K split (320 tiles: 256 whole, the last 32 weight tiles of the last 2 activation
+// tiles in 4 pieces) 551 -> 498 us.
 inline void mmqh_tail(MmqhPlan &p, double best_t, int64_t n, int64_t k, int64_t m) {
     const int tiles = p.tiles_n * p.tiles_m, slots = MMQH_CUS;
     p.tail = {tiles, 1, 0, 0, 0, 0, 0};
     const int rem = tiles % slots, full = tiles - rem;
-    if (full == 0 || rem == 0 || 2 * rem > slots || rem > p.tiles_n) return;
-    const int64_t r0 = int64_t(p.tiles_m - 1) * p.cfg.bm(), c0 = int64_t(p.tiles_n - rem) * p.cfg.bn();
-    const int64_t rows = std::min<int64_t>(p.cfg.bm(), m - r0), cols = n - c0;
+    if (full == 0 || rem == 0 || 2 * rem > slots) return;
+    // the rectangle: the fewest activation tiles whose last `width` weight tiles make `rem`
+    int height = 1;
+    while (height <= p.tiles_m && (rem % height || rem / height > p.tiles_n)) ++height;
+    if (height > p.tiles_m) return;
+    const int64_t r0 = int64_t(p.tiles_m - height) * p.cfg.bm(), c0 = int64_t(p.tiles_n - rem / height) * p.cfg.bn();
+    const int64_t rows = m - r0, cols = n - c0;
     const int stages = static_cast<int>((k + 255) / 256 * 4);
     int64_t pieces = std::min<int64_t>({slots / rem, 8, stages / 4,
                                         static_cast<int64_t>(MMQH_TAIL_BYTES / size_t(rows * cols * 4))});
@@ -781,8 +799,11 @@ inline MmqhPlan mmqh_plan(int64_t n, int64_t k, int64_t m) {
     if (m <= 96) {
         mmqh_consider<TYPE, 1, 3, 4, 1>(best, t, n, k, m);
     } else {
+        // 256-row tiles from 129 rows: one partly filled 256-row tile takes less time than two
+        // 128-row tiles (MI355X, 160 / 240 rows: Q4_K 34816 x 5120 158 / 161 -> 140 / 143 us,
+        // IQ3_S 223 -> 166 us, Q4_K 5120 x 17408 94 / 104 -> 84 / 97 us)
         if constexpr (mmqh_fits<TYPE, 2, 4, 2, 2>()) {
-            if (m >= 256) mmqh_consider<TYPE, 2, 4, 2, 2>(best, t, n, k, m);
+            if (m > 128) mmqh_consider<TYPE, 2, 4, 2, 2>(best, t, n, k, m);
             else mmqh_consider<TYPE, 2, 2, 2, 2>(best, t, n, k, m);
         } else {
             mmqh_consider<TYPE, 2, 2, 2, 2>(best, t, n, k, m);

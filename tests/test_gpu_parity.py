@@ -4,7 +4,7 @@ Bars: activation bytes bit-exact (the decode path's Q8_1 blocks, and the batched
 GGML MMQ planes read back from the scratch); GEMV/GEMM outputs within 1e-3 normwise
 max-rel (max|y - ref| / max|ref| per activation row) of the oracle's FP64 result for F32
 output, and within 2^-8 for BF16 output (bf16 keeps 8 significant bits, so rounding alone
-reaches 2^-9 of max|y|). Up to 8 rows the reference is the decode arithmetic
+reaches 2^-9 of max|y|, and up to 2^-8 where max|y| sits just above a power of two). Up to 8 rows the reference is the decode arithmetic
 (oracle_prepare + oracle_mul_mat); above 8 rows it is the batched path's
 (oracle_prepare_mmq + oracle_mul_mat_mmq, O.mmq_reference).
 """
@@ -531,20 +531,22 @@ def test_batched_prefill_tiles(kai, qtype, weights, m, n, k):
     assert err <= TOL_F32
 
 
-# More tiles than CUs with a short last round: the last tiles (inside the last activation tile)
-# run in K pieces whose sums a second kernel adds into that rectangle of the output, in place of
-# an unsplit plan's short round or a K split's extra rounds. Q4_K on 256 x 128 tiles: 2 x 141
-# tiles, the last 26 in 4 pieces of one 256-value step, the rectangle rows 256..299 by 3280
-# columns (the last tile 80 wide); Q2_K on 128 x 128 tiles: 3 x 86 tiles, the last 2 in 8
-# pieces, the rectangle 4 rows by 248 columns; Q4_0 at 40 rows on 128 x 96 tiles and IQ3_S at
-# 120 rows on 128 x 128 tiles: 258 tiles, the last 2 (232 columns, the last tile 104 wide) in 4
-# pieces over every row.
-TAIL = [(O.Q4_K, 300, 18000, 1024, 256), (O.Q2_K, 260, 11000, 2048, 256), (O.Q4_0, 40, 33000, 1024, 0),
-        (O.IQ3_S, 120, 33000, 1024, 0)]
+# More tiles than CUs with a short last round: the tiles of a rectangle at the output's end run
+# in K pieces whose sums a second kernel adds into that rectangle, in place of an unsplit plan's
+# short round or a K split's extra rounds; the other tiles run whole. Rectangles (rows r0.., weight
+# rows c0..): Q4_K on 256 x 128 tiles, 2 x 141 tiles, the last 26 in 4 pieces of one 256-value
+# step (the last tile 80 wide); Q2_K on 128 x 128 tiles, 3 x 86 tiles, the last 2 in 8 pieces (4
+# rows); Q4_0 at 40 rows on 128 x 96 tiles and IQ3_S at 120 rows on 128 x 128 tiles, 258 tiles,
+# the last 2 in 4 pieces over every row; two activation tiles high: Q2_K 27 x 10 tiles of 128 x
+# 128, the last 7 weight tiles of the last 2 (226 rows, the last tile 100 wide) in 4 pieces, and
+# Q4_K 14 x 20 tiles of 256 x 128, the last 12 of the last 2 (412 rows) in 2 pieces.
+TAIL = [(O.Q4_K, 300, 18000, 1024, 256, 14720), (O.Q2_K, 260, 11000, 2048, 256, 10752),
+        (O.Q4_0, 40, 33000, 1024, 0, 32768), (O.IQ3_S, 120, 33000, 1024, 0, 32768),
+        (O.Q2_K, 3426, 1252, 1024, 3200, 384), (O.Q4_K, 3484, 2500, 512, 3072, 1024)]
 
 
-@pytest.mark.parametrize("qtype,m,n,k,r0", TAIL, ids=[f"{O.NAMES[t]}-{m}x{n}x{k}" for t, m, n, k, _ in TAIL])
-def test_batched_tail_tiles_in_k_pieces(kai, qtype, m, n, k, r0):
+@pytest.mark.parametrize("qtype,m,n,k,r0,c0", TAIL, ids=[f"{O.NAMES[t]}-{m}x{n}x{k}" for t, m, n, k, _, _ in TAIL])
+def test_batched_tail_tiles_in_k_pieces(kai, qtype, m, n, k, r0, c0):
     print(f"batched tail tiles {O.NAMES[qtype]} m={m} n={n} k={k}", flush=True)
     rng = np.random.default_rng(qtype + m)
     w = O.random_blocks(qtype, n, k, rng)
@@ -552,14 +554,15 @@ def test_batched_tail_tiles_in_k_pieces(kai, qtype, m, n, k, r0):
     ref = O.mmq_reference(qtype, w, x, threads=16)
     mats = [(qtype, w, to_dev(w))]
     out = gpu_mmq(kai, mats, to_dev(x)).cpu().numpy()
-    c0 = n - 232 if r0 == 0 else 0
     assert O.normwise_rel(out, ref) <= TOL_F32
     assert O.normwise_rel(out[r0:, c0:], ref[r0:, c0:]) <= TOL_F32
+    assert O.normwise_rel(out[:, :c0], ref[:, :c0]) <= TOL_F32
     again = gpu_mmq(kai, mats, to_dev(x)).cpu().numpy()
     assert np.array_equal(out, again), "the pieces are added in a fixed order"
     outb = gpu_mmq(kai, mats, to_dev(x), bf16=True, stride=n + 3).float().cpu().numpy()
-    assert O.normwise_rel(outb[:, :n], ref) <= TOL_BF16
-    # the same sums as the f32 output, rounded to nearest even once (pieces and whole tiles)
+    # the same sums as the f32 output (checked above), rounded to nearest even once, pieces and
+    # whole tiles alike (over thousands of rows some row's maximum sits just above a power of
+    # two, where that rounding alone approaches TOL_BF16)
     assert np.array_equal(outb[:, :n], torch.from_numpy(out).to(torch.bfloat16).float().numpy())
     assert np.isnan(outb[:, n:]).all()
 
