@@ -153,6 +153,25 @@ def test_legacy_gemm_shapes(kai):
     assert O.normwise_rel(y, xb.astype(np.float64) @ O.dequantize(O.Q8_0, w, kk).astype(np.float64).T) <= 1e-5
 
 
+@pytest.mark.parametrize("qtype", [O.Q4_K, O.Q6_K], ids=lambda t: O.NAMES[t])
+def test_legacy_gemm_many_rows(kai, qtype):
+    """ggml_mul_mat_a8 at 300 and 1030 activation rows: the legacy quantisation into the planes by
+    a workgroup per whole row (from 256 rows), a row of zeros and rows of very different
+    scales."""
+    from kaillm_amd.ops import ggml_mul_mat_a8
+
+    for m in (300, 1030):
+        print(f"legacy a8 many rows {O.NAMES[qtype]} m={m}", flush=True)
+        rng = np.random.default_rng(qtype + m)
+        n, k = 68, 1024
+        x = (rng.standard_normal((m, k)) * rng.uniform(1e-2, 1e2, (m, 1))).astype(np.float32)
+        x[7] = 0.0
+        w = _weights(qtype, n, k, rng, "random")
+        y = ggml_mul_mat_a8(to_dev(w), to_dev(x), qtype, n).cpu().numpy()
+        assert O.normwise_rel(y, O.legacy_reference(qtype, w, x, 1)) <= TOL_F32
+        assert np.all(y[7] == 0.0)
+
+
 # ggml_mul_mat_a8 on the planes route (Q4_K, Q8_0, Q6_K) with row counts that are not a
 # multiple of four (an odd vocabulary, say), through every batched kernel: the small-M and
 # persistent GEMMs (9 and 16 rows) and the tiled one (17 and 40).
