@@ -560,15 +560,90 @@ __device__ __forceinline__ void prepare_mmq_chunk(const MmqPlanes &p, float (&v)
     }
 }
 
+// One workgroup per row (many rows): the thread loads its R runs of the row at once (run u
+// of thread t is run t + 256 u, the thread's run of chunk u), takes the row maximum from
+// them (and from the rest of a row longer than 2048 R values) and converts each chunk from
+// the kept values, so the row is read once (the runs of chunks from R on are read again).
+template <int DTYPE, bool LEGACY, int R>
+__device__ __forceinline__ void prepare_whole_row(const typename Src<DTYPE>::T *xr, int k, int m, int row, int chunks,
+                                                  float *lds, const MmqPlanes &p, int kpad_blocks, int hblocks,
+                                                  int mpad) {
+    const int runs = k / 8, nblocks = k / QK8_1, part = threadIdx.x & 3, t = threadIdx.x;
+    Raw8<DTYPE> keep[R];
+    float mx = 0.0f;
+    if (row < m) {  // uniform over the workgroup
+#pragma unroll
+        for (int u = 0; u < R; ++u) load_raw8<DTYPE>(xr + 8 * min(t + u * PREP_THREADS, runs - 1), keep[u]);
+        if constexpr (!LEGACY) {
+#pragma unroll
+            for (int u = 0; u < R; ++u) {
+                float v[8];
+                convert8<DTYPE>(keep[u], v);
+                if (t + u * PREP_THREADS < runs) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[j]));
+                }
+            }
+            // the runs past the kept ones (rows longer than 2048 R values), four at a time
+            for (int u0 = R; u0 * PREP_THREADS < runs; u0 += 4) {
+                Raw8<DTYPE> r[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) load_raw8<DTYPE>(xr + 8 * min(t + (u0 + u) * PREP_THREADS, runs - 1), r[u]);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    float v[8];
+                    convert8<DTYPE>(r[u], v);
+                    if (t + (u0 + u) * PREP_THREADS < runs) {
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[j]));
+                    }
+                }
+            }
+        }
+    }
+    float scale = 1.0f;
+    if constexpr (LEGACY) {
+        if (row < m && t == 0) p.inverse[row] = 1.0f;
+    } else {
+        scale = row < m ? row_scale_from_max(block_max(mx, lds), p.inverse + row, t == 0) : 0.0f;
+    }
+#pragma clang loop unroll(full)  // keep[] stays in registers only with constant indices
+    for (int c = 0; c < R; ++c) {
+        if (c < chunks) {  // uniform
+            const int ib = c * PREP_BLOCKS + (t >> 2);
+            float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+            if (row < m && ib < nblocks) convert8<DTYPE>(keep[c], v);
+            prepare_mmq_chunk<LEGACY>(p, v, scale, ib, row, part, k, m, nblocks, kpad_blocks, hblocks, mpad);
+        }
+    }
+    for (int c = R; c < chunks; ++c) {
+        const int ib = c * PREP_BLOCKS + (t >> 2);
+        float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        if (row < m && ib < nblocks) load8<DTYPE>(xr + QK8_1 * ib + 8 * part, v);
+        prepare_mmq_chunk<LEGACY>(p, v, scale, ib, row, part, k, m, nblocks, kpad_blocks, hblocks, mpad);
+    }
+}
+
 template <int DTYPE, bool LEGACY>
 __global__ __launch_bounds__(PREP_THREADS) void prepare_mmq_kernel(
     const typename Src<DTYPE>::T *__restrict__ x, int64_t stride_x, int k, int m, int kpad_blocks, int hblocks, int mpad,
     MmqPlanes p, int chunks) {
     __shared__ float wave_max_lds[PREP_THREADS / WAVE];
-    const int row = blockIdx.x;  // images: rows m..15 are written as zeros
+    // images: rows m..15 (m..mpad) are written as zeros. Workgroups are dealt round-robin over
+    // the 8 XCDs: each XCD takes a contiguous range of rows, so the rows that share a line of
+    // the images and planes (32-byte pieces of adjacent rows at one K position) are written
+    // into one L2, where the pieces merge before the line goes to HBM.
+    const int row = gridDim.x % 8 ? blockIdx.x : (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;
     const int nblocks = k / QK8_1;
     const int part = threadIdx.x & 3;
     const auto *xr = x + static_cast<int64_t>(row) * stride_x;
+    if (chunks > 1) {  // one workgroup per row, all its chunks (uniform over the grid)
+        if (k <= 4 * 8 * PREP_THREADS)
+            prepare_whole_row<DTYPE, LEGACY, 4>(xr, k, m, row, chunks, wave_max_lds, p, kpad_blocks, hblocks, mpad);
+        else
+            prepare_whole_row<DTYPE, LEGACY, 12>(xr, k, m, row, chunks, wave_max_lds, p, kpad_blocks, hblocks, mpad);
+        return;
+    }
     float own[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
     float scale = 0.0f;
     if constexpr (LEGACY) {
@@ -577,20 +652,17 @@ __global__ __launch_bounds__(PREP_THREADS) void prepare_mmq_kernel(
     } else if (row < m) {  // uniform over the workgroup
         scale = row_scale<DTYPE>(xr, k, wave_max_lds, p.inverse + row, blockIdx.y == 0 && threadIdx.x == 0, own);
     }
-    // chunks of PREP_BLOCKS blocks: the workgroup's first from the row maximum's pass (own), the
-    // others read again (from L2)
-    for (int c = 0; c < chunks; ++c) {
-        const int ib = (blockIdx.y * chunks + c) * PREP_BLOCKS + (threadIdx.x >> 2);
-        float v[8];
+    // the workgroup's chunk of PREP_BLOCKS blocks, from the row maximum's pass (own)
+    const int ib = blockIdx.y * PREP_BLOCKS + (threadIdx.x >> 2);
+    float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = own[j];
-        if (LEGACY || c > 0) {
+    for (int j = 0; j < 8; ++j) v[j] = own[j];
+    if (LEGACY) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = 0.0f;
-            if (row < m && ib < nblocks) load8<DTYPE>(xr + QK8_1 * ib + 8 * part, v);
-        }
-        prepare_mmq_chunk<LEGACY>(p, v, scale, ib, row, part, k, m, nblocks, kpad_blocks, hblocks, mpad);
+        for (int j = 0; j < 8; ++j) v[j] = 0.0f;
+        if (row < m && ib < nblocks) load8<DTYPE>(xr + QK8_1 * ib + 8 * part, v);
     }
+    prepare_mmq_chunk<LEGACY>(p, v, scale, ib, row, part, k, m, nblocks, kpad_blocks, hblocks, mpad);
 }
 
 template <int DTYPE>

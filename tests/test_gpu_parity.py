@@ -326,12 +326,14 @@ def small_m_image(plane, layout, k):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("m,k", [(9, 256), (12, 2080), (16, 4096), (17, 1056), (80, 5120), (130, 2080), (300, 2080),
-                                 (1030, 4096)])
+                                 (1030, 4096), (260, 17408), (256, 32768)])
 def test_mmq_planes_bit_exact(kai, dtype, m, k):
     """The batched path's activation (row scale + GGML MMQ quantisation into D4, DS4 and
     D2S6 planes, K padded to 512) read back from the scratch equals the oracle's bytes, in the
     form the GEMMs read it: up to 16 rows the small-M images of the planes, above 16 rows the
-    fp16 GEMM's images (h_image_parts); from 256 rows (image rows) a workgroup walks a whole row."""
+    fp16 GEMM's images (h_image_parts); from 256 rows (image rows) a workgroup walks a whole row,
+    converting up to 12 chunks from the values of its row-maximum pass (K = 32768: 16 chunks, the
+    last 4 read again)."""
     print(f"mmq planes dtype={dtype} m={m} k={k}", flush=True)
     rng = np.random.default_rng(m + k)
     kq = k if k % 256 == 0 else None
