@@ -141,12 +141,13 @@ int kai_fused_mmvq(const void *weight, int type, int64_t n, int64_t k, int64_t m
  * sharing k, at m > 8 activation rows: [inverse: m floats][one int8 activation region per
  * layout read by a matrix on the int8 kernels, D4 then DS4 then D2S6][one fp16 image
  * (codes, then min-pass sums) per layout read by a matrix on the fp16 GEMM][the fp32
- * partial sums of a kernel that splits K], each region padded to 256 bytes. Up to 16 rows
+ * partial sums of a kernel that splits K, or of the K pieces the fp16 GEMM runs its last
+ * tiles in (at most 32 MiB)], each region padded to 256 bytes. Up to 16 rows
  * the int8 region is the small-M image (the GGML MMQ quantisation laid out for the small-M
  * GEMM's LDS, 4608 bytes (D4) or 5632 bytes (DS4, D2S6) per 256 values of k) and the
  * partial sums the small-M GEMM's (16 x 16 values per piece of a 16-row set). Above 16 rows
  * a matrix runs on the fp16 GEMM when mmq_uses_h(type, m, rows) holds (every type but
- * Q6_K, except more than 16384 rows up to 96 rows), reading the fp16 image: codes
+ * Q6_K), reading the fp16 image: codes
  * half(d * q) as [k padded to 256 / 16][m padded to 32][16], and per 256 values of k and row
  * 64 (DS4) or 128 (D2S6) bytes of min-pass sums (none for D4); the others read a plane:
  * 128-value blocks of 144 bytes in [k/128][m] order with k padded to 512. The size is not
