@@ -574,6 +574,28 @@ def test_batched_tail_tiles_in_k_pieces(kai, qtype, m, n, k, r0, c0):
     assert np.isnan(outb[:, n:]).all()
 
 
+def test_batched_tail_in_a_group_with_unaligned_columns(kai):
+    """A group whose first matrix has a tail of K pieces over 234 columns (33002 rows: 258
+    tiles of 128, the last 2 in pieces) and whose second starts at an even but not 16-byte
+    aligned column: the pieces' sums and their reduction take the element-wise paths. (Both
+    Q4_0: random Q8_0 blocks give outputs several times larger, and two such columns would set
+    each row's maximum, making the normwise bound a bound on single outputs.)"""
+    print("batched tail in an unaligned group", flush=True)
+    rng = np.random.default_rng(33002)
+    m, k = 40, 1024
+    w1 = O.random_blocks(O.Q4_0, 33002, k, rng)
+    w2 = O.random_blocks(O.Q4_0, 2, k, rng)
+    mats = [(O.Q4_0, w1, to_dev(w1)), (O.Q4_0, w2, to_dev(w2))]
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    ref = batched_ref(mats, x, threads=16)
+    out = gpu_mmq(kai, mats, to_dev(x)).cpu().numpy()
+    assert O.normwise_rel(out, ref) <= TOL_F32
+    assert O.normwise_rel(out[:, 32768:], ref[:, 32768:]) <= TOL_F32
+    outb = gpu_mmq(kai, mats, to_dev(x), bf16=True, stride=33004 + 5).float().cpu().numpy()
+    assert np.array_equal(outb[:, :33004], torch.from_numpy(out).to(torch.bfloat16).float().numpy())
+    assert np.isnan(outb[:, 33004:]).all()
+
+
 def test_batched_heavy_tailed_activations_bf16_out_and_stride(kai):
     """Activations spread over many binades (small-scale blocks beside large ones) and
     exact zeros; bf16 output into a wider matrix, the padding left untouched."""
