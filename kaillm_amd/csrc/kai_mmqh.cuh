@@ -224,7 +224,8 @@ template <> struct MmqhW<Q4_K> {
 // codes c - 2 are -2..1, so the folded values are exact. WMIN row: [-mw_0..15 | 2 dw_0..15]
 // against the activation's [Shi | Slo] and [Xhi | Xlo].
 template <> struct MmqhW<Q2_K> {
-    static constexpr int SEG = 84, RS = 112, C0 = 2;
+    // raw rows of 96 bytes (84 wire bytes): the 256-row tile's LDS then fits in 160 KiB
+    static constexpr int SEG = 84, RS = 96, C0 = 2;
     static __device__ void convert(const lds_u8 *seg, int j4, int h, int, const uint32_t *, uint4 (&o)[4]) {
         const int kb = 2 * j4 + h, sh = 2 * (kb % 4);
         const uint4 q0 = load_unaligned<uint4>(seg + 16 + 32 * (kb / 4)),

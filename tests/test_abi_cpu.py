@@ -155,14 +155,14 @@ def test_mmq_workspace_holds_the_tail_pieces(kai):
     those last tiles (inside the last activation tile) run in K pieces (at most 8, whole
     256-value steps, as many as the idle CUs take), whose sums are pieces x rows x columns
     fp32. Q4_K 18000 x 1024 at 300 rows: 2 x 141 tiles of 256 x 128, the last 26 in 4 pieces
-    over rows 256..299 and columns 14720..17999; Q2_K 11000 x 2048 at 260 rows: 3 x 86 tiles of
-    128 x 128, the last 2 in 8 pieces over rows 256..259 and columns 10752..10999; in place of a
+    over rows 256..299 and columns 14720..17999, and Q2_K the same (its 256-row tile fits the
+    LDS with 96-byte raw rows); in place of a
     K split, Q4_0 and IQ3_S 33000 x 1024 at 40 and 120 rows: 258 tiles of 128 weight rows, the
     last 2 in 4 pieces over every row and columns 32768..32999; two activation tiles high, Q4_K
     5120 x 17408 at 2048 rows (8 x 40 tiles of 256 x 128, in place of a four-way K split): the
     last 32 weight tiles of the last 2 in 4 pieces, rows 1536..2047 by columns 1024..5119."""
     a256 = lambda b: (b + 255) // 256 * 256
-    for qtype, n, k, m, pieces in ((O.Q4_K, 18000, 1024, 300, 4 * 44 * 3280), (O.Q2_K, 11000, 2048, 260, 8 * 4 * 248),
+    for qtype, n, k, m, pieces in ((O.Q4_K, 18000, 1024, 300, 4 * 44 * 3280), (O.Q2_K, 18000, 1024, 300, 4 * 44 * 3280),
                                    (O.Q4_0, 33000, 1024, 40, 4 * 40 * 232), (O.IQ3_S, 33000, 1024, 120, 4 * 120 * 232),
                                    (O.Q4_K, 5120, 17408, 2048, 4 * 512 * 4096)):
         types = (ctypes.c_int * 1)(qtype)

@@ -542,14 +542,13 @@ def test_batched_prefill_tiles(kai, qtype, weights, m, n, k):
 # in K pieces whose sums a second kernel adds into that rectangle, in place of an unsplit plan's
 # short round or a K split's extra rounds; the other tiles run whole. Rectangles (rows r0.., weight
 # rows c0..): Q4_K on 256 x 128 tiles, 2 x 141 tiles, the last 26 in 4 pieces of one 256-value
-# step (the last tile 80 wide); Q2_K on 128 x 128 tiles, 3 x 86 tiles, the last 2 in 8 pieces (4
-# rows); Q4_0 at 40 rows on 128 x 96 tiles and IQ3_S at 120 rows on 128 x 128 tiles, 258 tiles,
-# the last 2 in 4 pieces over every row; two activation tiles high: Q2_K 27 x 10 tiles of 128 x
-# 128, the last 7 weight tiles of the last 2 (226 rows, the last tile 100 wide) in 4 pieces, and
-# Q4_K 14 x 20 tiles of 256 x 128, the last 12 of the last 2 (412 rows) in 2 pieces.
-TAIL = [(O.Q4_K, 300, 18000, 1024, 256, 14720), (O.Q2_K, 260, 11000, 2048, 256, 10752),
-        (O.Q4_0, 40, 33000, 1024, 0, 32768), (O.IQ3_S, 120, 33000, 1024, 0, 32768),
-        (O.Q2_K, 3426, 1252, 1024, 3200, 384), (O.Q4_K, 3484, 2500, 512, 3072, 1024)]
+# step (the last tile 80 wide); Q4_0 at 40 rows on 128 x 96 tiles and IQ3_S and Q2_K at 120 rows
+# on 128 x 128 tiles, 258 tiles, the last 2 (232 columns, the last tile 104 wide) in 4 pieces
+# over every row; two activation tiles high: Q4_K and Q2_K, 14 x 20 tiles of 256 x 128, the last
+# 12 of the last 2 (412 rows, the last tile 68 wide) in 2 pieces.
+TAIL = [(O.Q4_K, 300, 18000, 1024, 256, 14720), (O.Q4_0, 40, 33000, 1024, 0, 32768),
+        (O.IQ3_S, 120, 33000, 1024, 0, 32768), (O.Q2_K, 120, 33000, 1024, 0, 32768),
+        (O.Q4_K, 3484, 2500, 512, 3072, 1024), (O.Q2_K, 3484, 2500, 512, 3072, 1024)]
 
 
 @pytest.mark.parametrize("qtype,m,n,k,r0,c0", TAIL, ids=[f"{O.NAMES[t]}-{m}x{n}x{k}" for t, m, n, k, _, _ in TAIL])
