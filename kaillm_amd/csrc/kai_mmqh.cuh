@@ -224,8 +224,7 @@ template <> struct MmqhW<Q4_K> {
 // codes c - 2 are -2..1, so the folded values are exact. WMIN row: [-mw_0..15 | 2 dw_0..15]
 // against the activation's [Shi | Slo] and [Xhi | Xlo].
 template <> struct MmqhW<Q2_K> {
-    // raw rows of 96 bytes (84 wire bytes): the 256-row tile's LDS then fits in 160 KiB
-    static constexpr int SEG = 84, RS = 96, C0 = 2;
+    static constexpr int SEG = 84, RS = 112, C0 = 2;
     static __device__ void convert(const lds_u8 *seg, int j4, int h, int, const uint32_t *, uint4 (&o)[4]) {
         const int kb = 2 * j4 + h, sh = 2 * (kb % 4);
         const uint4 q0 = load_unaligned<uint4>(seg + 16 + 32 * (kb / 4)),
@@ -263,9 +262,16 @@ template <int TYPE> constexpr bool mmqh_type() {
 // Min-pass operand bytes per activation row and superblock (0: none).
 template <int TYPE> constexpr int mmqh_amin_bytes() { return TYPE == Q4_K ? 64 : TYPE == Q2_K ? 128 : 0; }
 
+// Raw LDS row stride of a tile: the format's, but 96 bytes for Q2_K's 256-row tile, whose LDS
+// then fits in 160 KiB (the 112-byte rows spread a quarter-wave's 16-byte reads over every bank:
+// Q2_K 34816 x 5120 at 40-120 rows 2-4 % faster than with 96)
+template <int TYPE, int BM>
+constexpr int mmqh_rs() {
+    return TYPE == Q2_K && BM == 256 ? 96 : MmqhW<TYPE>::RS;
+}
 template <int TYPE, int BN, int BM>
 struct MmqhLds {
-    static constexpr int ASTAGE = 128 * BM, WSTAGE = 128 * BN, RAW = BN * MmqhW<TYPE>::RS;
+    static constexpr int ASTAGE = 128 * BM, WSTAGE = 128 * BN, RAW = BN * mmqh_rs<TYPE, BM>();
     static constexpr int WMIN = MmqhW<TYPE>::C0 ? 64 * BN : 16;
     static constexpr int AMIN = mmqh_amin_bytes<TYPE>() ? mmqh_amin_bytes<TYPE>() * BM : 16;
     static constexpr int TOTAL = 2 * ASTAGE + 2 * WSTAGE + 2 * RAW + WMIN + AMIN + (TYPE == IQ3_S ? 2048 : 0);
@@ -298,6 +304,7 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
     constexpr int CW = GN * GM, THREADS = 64 * CW, BN = 32 * WN * GN, BM = 32 * WM * GM;
     constexpr int AB = mmqh_amin_bytes<TYPE>();
     constexpr bool SHORT = block_elems(TYPE) == 32;  // K may end inside a step
+    constexpr int RS = mmqh_rs<TYPE, BM>();           // raw LDS row stride
     using L = MmqhLds<TYPE, BN, BM>;
     constexpr int UNITS = 2 * BN, UPT = UNITS / THREADS;  // weight units per producer thread and stage
     static_assert(UNITS % THREADS == 0 && (8 * BM) % THREADS == 0, "whole units and copies per producer thread");
@@ -370,7 +377,7 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
         for (int p = 0; p < UPT; ++p) {
             const int u = ctid + p * THREADS, j = u % BN, h = u / BN;
             uint4 c[4];
-            W::convert(rb + j * W::RS, s & 3, h, valid, grid_lds, c);
+            W::convert(rb + j * RS, s & 3, h, valid, grid_lds, c);
             store16(wb + (2 * h) * BN * 32 + mmqh_swz(j, 0), c[0]);
             store16(wb + (2 * h) * BN * 32 + mmqh_swz(j, 1), c[1]);
             store16(wb + (2 * h + 1) * BN * 32 + mmqh_swz(j, 0), c[2]);
@@ -378,7 +385,7 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
             if constexpr (W::C0 != 0) {
                 if constexpr (decltype(first)::value) {
                     uint4 o0, o1;
-                    W::mins(rb + j * W::RS, h, o0, o1);
+                    W::mins(rb + j * RS, h, o0, o1);
                     store16(wmin + j * 64 + 32 * h, o0);
                     store16(wmin + j * 64 + 32 * h + 16, o1);
                 }
@@ -393,7 +400,7 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
             for (int p = 0; p < UPT; ++p) {
                 const int u = ctid + p * THREADS, j = u % BN, h = u / BN;
                 uint4 o0, o1;
-                W::mins(rb + j * W::RS, h, o0, o1);
+                W::mins(rb + j * RS, h, o0, o1);
                 store16(wmin + j * 64 + 32 * h, o0);
                 store16(wmin + j * 64 + 32 * h + 16, o1);
             }
@@ -412,7 +419,7 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
         for (int p = 0; p < RPT; ++p) {
             const int c = min(ptid + p * THREADS, RAWC - 1), r = c / CPR;
             raw_row[p] = weight + int64_t(min(n0 + r, n - 1)) * row_bytes;
-            raw_at[p] = r * W::RS;
+            raw_at[p] = r * RS;
             raw_piece[p] = 16 * (c % CPR);
         }
         const int nblocks = k / QK8_1;
@@ -437,7 +444,7 @@ __global__ __launch_bounds__(128 * GN * GM) __attribute__((amdgpu_waves_per_eu(2
         // lane order and go straight from global memory to LDS, as the activation does (below).
         // The last copy index may end inside the waves; RAWC is a whole number of waves, so a wave
         // issues all of a copy index or none of it.
-        constexpr bool RAW_DMA = !SHORT && W::SEG == W::RS && W::SEG % 16 == 0;
+        constexpr bool RAW_DMA = !SHORT && W::SEG == RS && W::SEG % 16 == 0;
         static_assert(!RAW_DMA || RAWC % WAVE == 0, "whole waves of wire-byte copies");
         const int pwave = __builtin_amdgcn_readfirstlane(ptid / WAVE);
         const bool raw_all = RAWC % THREADS == 0 || (RPT - 1) * THREADS + WAVE * pwave < RAWC;  // uniform
